@@ -1,0 +1,94 @@
+/*
+ * zeno_amd_ext.h — extension entry points of libzeno (MI355X build).
+ *
+ * None of these exist in the reference (Lulzx/zeno); they sit beside the reference ABI of
+ * zeno.h and serve three callers:
+ *   - inspection of the model a world was built from (tests and the CPU oracle read the
+ *     constraint templates, colours and records the kernels use), without a GPU;
+ *   - device-resident stepping and timing for benchmarks and graph capture;
+ *   - solver state that the reference keeps but never exposes (lambda, previous contact
+ *     count), used by parity tests.
+ */
+#ifndef ZENO_AMD_EXT_H
+#define ZENO_AMD_EXT_H
+
+#include <stdint.h>
+
+#include "zeno.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ZenoAmdModelHandle;
+
+/* A parsed scene and the records the step reads. Pointers stay valid until the model (or
+ * world) is destroyed. Record layouts are the reference's GPU layouts:
+ * bodies 80 B (world.zig:1573-1597), joints 80 B (world.zig:1599-1620),
+ * geoms 64 B (primitives.zig:424-442), actuators 32 B (world.zig:1622-1637),
+ * sensors 32 B (sensors.zig:149-161), constraint templates 96 B (xpbd.zig:50-121). */
+typedef struct {
+    uint32_t num_bodies, num_joints, num_geoms, num_actuators, num_sensors, obs_dim;
+    uint32_t num_constraints, num_colors, max_color_size, num_pairs;
+    float timestep;      /* MJCF <option timestep> */
+    float gravity[3];
+    float friction, restitution, baumgarte, slop;
+    const void* bodies;
+    const void* joints;
+    const void* geoms;
+    const void* actuators;
+    const void* sensors;
+    const void* constraints;          /* colour-sorted templates (env 0) */
+    const uint32_t* color_ranges;     /* [num_colors][2] = (offset, count) */
+    const uint32_t* pairs;            /* [num_pairs] = g | g' << 16, broad-phase candidates */
+    const uint8_t* joint_limited;     /* [num_joints] JointDef.limited */
+    const float* init_positions;      /* [num_bodies*4] initial state of every env */
+    const float* init_quaternions;
+    const float* init_velocities;
+    const float* init_angular_velocities;
+    const float* inv_mass_inertia;    /* [num_bodies*4] */
+} ZenoAmdModelView;
+
+/* Parse MJCF and build the model on the host only (no GPU needed). NULL on failure; the
+ * reason is available from zeno_amd_last_error(). */
+ZenoAmdModelHandle zeno_amd_model_create(const char* mjcf_path);
+ZenoAmdModelHandle zeno_amd_model_create_from_string(const char* mjcf_string);
+void zeno_amd_model_destroy(ZenoAmdModelHandle model);
+int zeno_amd_model_view(ZenoAmdModelHandle model, ZenoAmdModelView* out);
+
+/* The model a world runs. */
+int zeno_amd_world_model_view(ZenoWorldHandle world, ZenoAmdModelView* out);
+
+/* Message of the last failure on this thread ("" when none). */
+const char* zeno_amd_last_error(void);
+
+/* Number of GPUs HIP reports (0 when none or when the runtime is unavailable). */
+int zeno_amd_device_count(void);
+
+/* Solver state that the reference keeps in device buffers without a getter:
+ * lambda per env and constraint (XPBDConstraint.state.x == state.y after every step),
+ * and prev_contact_counts. Copies into caller memory; returns 0 or an error code. */
+int zeno_amd_world_get_lambda(ZenoWorldHandle world, float* out /* [E*N] */);
+int zeno_amd_world_get_prev_contact_counts(ZenoWorldHandle world, uint32_t* out /* [E] */);
+
+/* Step with actions already in device memory (d_actions: [E*A] floats on the world's
+ * device). Same semantics as zeno_world_step. */
+int zeno_amd_world_step_device(ZenoWorldHandle world, const float* d_actions, uint32_t substeps);
+
+/* Waits for all work queued on the world's stream. */
+int zeno_amd_world_synchronize(ZenoWorldHandle world);
+
+/* Kernel timing with HIP events on the world's stream. enable != 0 starts recording an
+ * event pair around every step launch; get returns the summed kernel time in ms and the
+ * number of launches since the last reset (waits for the stream). */
+int zeno_amd_world_set_kernel_timing(ZenoWorldHandle world, int enable);
+int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, uint64_t* launches);
+
+/* Launch configuration chosen for the world: environments per wavefront and LDS bytes
+ * per workgroup. */
+int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZENO_AMD_EXT_H */

@@ -1,0 +1,197 @@
+"""Python driver for the CPU oracle (liboracle: zeno_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, never by the product. It steps a batch of environments on the CPU with the
+scalar restatement of the reference's step, on state arrays in the reference's layouts.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+from typing import Any, Dict, Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libzeno_oracle.so"
+
+CONTACT_DTYPE = np.dtype([("position_pen", "4f4"), ("normal_friction", "4f4"), ("indices", "4u4"),
+                          ("impulses", "4f4")])
+CONSTRAINT_DTYPE = np.dtype([("indices", "4u4"), ("anchor_a", "4f4"), ("anchor_b", "4f4"),
+                             ("axis_target", "4f4"), ("limits", "4f4"), ("state", "4f4")])
+
+
+class ZoModel(C.Structure):
+    _fields_ = [
+        ("num_envs", C.c_uint32), ("num_bodies", C.c_uint32), ("num_joints", C.c_uint32),
+        ("num_geoms", C.c_uint32), ("num_actuators", C.c_uint32), ("num_sensors", C.c_uint32),
+        ("obs_dim", C.c_uint32), ("num_constraints", C.c_uint32), ("num_colors", C.c_uint32),
+        ("max_contacts", C.c_uint32), ("contact_iterations", C.c_uint32), ("config_substeps", C.c_uint32),
+        ("timestep", C.c_float), ("gravity", C.c_float * 3),
+        ("friction", C.c_float), ("restitution", C.c_float), ("baumgarte", C.c_float), ("slop", C.c_float),
+        ("bodies", C.c_void_p), ("joints", C.c_void_p), ("geoms", C.c_void_p), ("actuators", C.c_void_p),
+        ("sensors", C.c_void_p), ("color_ranges", C.c_void_p),
+    ]
+
+
+class ZoState(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "positions", "quaternions", "velocities", "angular_velocities", "accelerations", "inv_mass_inertia",
+        "forces", "torques", "prev_positions", "prev_quaternions", "prev_velocities",
+        "joint_positions", "joint_velocities", "joint_torques", "observations",
+        "contacts", "contact_counts", "prev_contacts", "prev_contact_counts", "constraints")]
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (build with python -m zeno_amd.build)")
+        lib = C.CDLL(str(LIB_PATH))
+        lib.zo_step.restype = C.c_int
+        lib.zo_step.argtypes = [C.POINTER(ZoModel), C.POINTER(ZoState), C.c_void_p, C.c_uint32,
+                                C.c_uint32, C.c_uint32, C.c_int]
+        lib.zo_build_templates.restype = C.c_uint32
+        lib.zo_build_templates.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32,
+                                           C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32)]
+        lib.zo_atan2f.restype = C.c_float
+        lib.zo_atan2f.argtypes = [C.c_float, C.c_float]
+        lib.zo_asinf.restype = C.c_float
+        lib.zo_asinf.argtypes = [C.c_float]
+        lib.zo_collide_env.restype = None
+        lib.zo_collide_env.argtypes = [C.POINTER(ZoModel), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        _lib = lib
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def build_templates(model: Dict[str, Any]):
+    """Recomputes constraint templates, colours and colour ranges from the joint records."""
+    lib = load()
+    J = model["num_joints"]
+    out = np.zeros(max(3 * J, 1), dtype=CONSTRAINT_DTYPE)
+    ranges = np.zeros(512, dtype=np.uint32)
+    ncol = C.c_uint32()
+    joints = np.ascontiguousarray(model["joints"])
+    limited = np.ascontiguousarray(model["joint_limited"], dtype=np.uint8)
+    bodies = np.ascontiguousarray(model["bodies"])
+    n = lib.zo_build_templates(_p(joints) if J else None, _p(limited) if J else None, J, _p(bodies),
+                               model["num_bodies"], _p(out), _p(ranges), C.byref(ncol))
+    return out[:n].copy(), ranges[: 2 * ncol.value].reshape(-1, 2).copy(), ncol.value
+
+
+class OracleWorld:
+    """A batch of environments in the reference's buffer layouts, stepped on the CPU."""
+
+    def __init__(self, model: Dict[str, Any], num_envs: int, timestep: float = 0.0,
+                 contact_iterations: int = 4, max_contacts_per_env: int = 64, substeps: int = 1):
+        self.lib = load()
+        self.model = model
+        E, B = num_envs, model["num_bodies"]
+        J, A, N = model["num_joints"], model["num_actuators"], model["num_constraints"]
+        Jp, Op, M = max(J, 1), max(model["obs_dim"], 1), max_contacts_per_env
+        self.E, self.B, self.J, self.A, self.N, self.M = E, B, J, A, N, M
+        self.timestep = float(timestep if timestep > 0 else model["timestep"])
+        self.gravity = list(model["gravity"])
+        self.contact_iterations = contact_iterations
+        self.substeps = substeps
+        f4 = lambda: np.zeros((E, B, 4), np.float32)
+        self.positions = np.ascontiguousarray(np.broadcast_to(model["init_positions"], (E, B, 4)), np.float32).copy()
+        self.quaternions = np.ascontiguousarray(np.broadcast_to(model["init_quaternions"], (E, B, 4)), np.float32).copy()
+        self.velocities = np.ascontiguousarray(np.broadcast_to(model["init_velocities"], (E, B, 4)), np.float32).copy()
+        self.angular_velocities = np.ascontiguousarray(np.broadcast_to(model["init_angular_velocities"], (E, B, 4)), np.float32).copy()
+        self.inv_mass_inertia = np.ascontiguousarray(np.broadcast_to(model["inv_mass_inertia"], (E, B, 4)), np.float32).copy()
+        self.accelerations, self.forces, self.torques = f4(), f4(), f4()
+        self.prev_positions, self.prev_quaternions, self.prev_velocities = f4(), f4(), f4()
+        self.joint_positions = np.zeros((E, Jp), np.float32)
+        self.joint_velocities = np.zeros((E, Jp), np.float32)
+        self.joint_torques = np.zeros((E, Jp), np.float32)
+        self.observations = np.zeros((E, Op), np.float32)
+        self.contacts = np.zeros((E, M), CONTACT_DTYPE)
+        self.contact_counts = np.zeros(E, np.uint32)
+        self.prev_contacts = np.zeros((E, M), CONTACT_DTYPE)
+        self.prev_contact_counts = np.zeros(E, np.uint32)
+        tmpl = model["constraints"]
+        self.constraints = np.ascontiguousarray(np.broadcast_to(tmpl, (E, N)), CONSTRAINT_DTYPE).copy()
+        if N:
+            self.constraints["indices"][:, :, 2] = np.arange(E, dtype=np.uint32)[:, None]
+        self._keep = {k: np.ascontiguousarray(model[k]) for k in
+                      ("bodies", "joints", "geoms", "actuators", "sensors")}
+        self._keep["color_ranges"] = np.ascontiguousarray(model["color_ranges"], dtype=np.uint32).reshape(-1)
+
+    def _model_struct(self) -> ZoModel:
+        m = self.model
+        zm = ZoModel()
+        zm.num_envs, zm.num_bodies, zm.num_joints = self.E, self.B, self.J
+        zm.num_geoms, zm.num_actuators, zm.num_sensors = m["num_geoms"], self.A, m["num_sensors"]
+        zm.obs_dim, zm.num_constraints, zm.num_colors = m["obs_dim"], self.N, m["num_colors"]
+        zm.max_contacts, zm.contact_iterations, zm.config_substeps = self.M, self.contact_iterations, self.substeps
+        zm.timestep = self.timestep
+        for i in range(3):
+            zm.gravity[i] = self.gravity[i]
+        zm.friction, zm.restitution = m["friction"], m["restitution"]
+        zm.baumgarte, zm.slop = m["baumgarte"], m["slop"]
+        k = self._keep
+        zm.bodies = _p(k["bodies"])
+        zm.joints = _p(k["joints"]) if self.J else None
+        zm.geoms = _p(k["geoms"]) if m["num_geoms"] else None
+        zm.actuators = _p(k["actuators"]) if self.A else None
+        zm.sensors = _p(k["sensors"]) if m["num_sensors"] else None
+        zm.color_ranges = _p(k["color_ranges"]) if k["color_ranges"].size else None
+        return zm
+
+    def _state_struct(self) -> ZoState:
+        s = ZoState()
+        for name, _ in ZoState._fields_:
+            setattr(s, name, _p(getattr(self, name)))
+        return s
+
+    def step(self, actions: Optional[np.ndarray], substeps: int = 0, env_begin: int = 0,
+             env_end: Optional[int] = None, nthreads: int = 0) -> None:
+        a = np.zeros((self.E, max(self.A, 1)), np.float32) if actions is None else \
+            np.ascontiguousarray(actions, np.float32).reshape(self.E, self.A)
+        if self.A == 0:
+            a = np.zeros((self.E, 1), np.float32)
+        zm, zs = self._model_struct(), self._state_struct()
+        end = self.E if env_end is None else env_end
+        self.lib.zo_step(C.byref(zm), C.byref(zs), _p(a), substeps, env_begin, end, nthreads)
+
+    def reset_to_state(self, positions, quaternions, velocities=None, angular_velocities=None, mask=None):
+        """main.zig:290-385: copy the given arrays for the selected envs; zero every count."""
+        sel = np.ones(self.E, bool) if mask is None else np.asarray(mask).astype(bool)
+        self.positions[sel] = np.asarray(positions, np.float32).reshape(self.E, self.B, 4)[sel]
+        self.quaternions[sel] = np.asarray(quaternions, np.float32).reshape(self.E, self.B, 4)[sel]
+        if velocities is not None:
+            self.velocities[sel] = np.asarray(velocities, np.float32).reshape(self.E, self.B, 4)[sel]
+        if angular_velocities is not None:
+            self.angular_velocities[sel] = np.asarray(angular_velocities, np.float32).reshape(self.E, self.B, 4)[sel]
+        self.contact_counts[:] = 0
+
+    def reset(self, mask=None):
+        """world.zig:1296-1314: restore the scene pose, zero joint q/qd, zero every count."""
+        sel = np.ones(self.E, bool) if mask is None else np.asarray(mask).astype(bool)
+        self.positions[sel] = self.model["init_positions"]
+        self.quaternions[sel] = self.model["init_quaternions"]
+        self.velocities[sel] = self.model["init_velocities"]
+        self.angular_velocities[sel] = self.model["init_angular_velocities"]
+        self.joint_positions[sel] = 0
+        self.joint_velocities[sel] = 0
+        self.contact_counts[:] = 0
+
+    def lambdas(self) -> np.ndarray:
+        return self.constraints["state"][:, :, 0].copy()
+
+
+def atan2f(y: float, x: float) -> float:
+    return load().zo_atan2f(y, x)
+
+
+def asinf(x: float) -> float:
+    return load().zo_asinf(x)

@@ -1,0 +1,118 @@
+// fp32 vector / quaternion helpers for the step kernel.
+//
+// Semantics follow the reference's MSL helpers (src/shaders/all_shaders.metal:76-100):
+// operations evaluate left to right, dot(a,b) = a.x*b.x + a.y*b.y + a.z*b.z,
+// length = sqrt(dot), quat_normalize divides each component by the length. The library is
+// compiled with -ffp-contract=off and correctly rounded division and square root, so each
+// expression rounds exactly as written.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace za {
+
+struct f3 { float x, y, z; };
+struct q4 { float x, y, z, w; };
+
+__device__ __forceinline__ f3 mk3(float x, float y, float z) { return {x, y, z}; }
+__device__ __forceinline__ q4 mk4(float x, float y, float z, float w) { return {x, y, z, w}; }
+__device__ __forceinline__ f3 add(f3 a, f3 b) { return {a.x + b.x, a.y + b.y, a.z + b.z}; }
+__device__ __forceinline__ f3 sub(f3 a, f3 b) { return {a.x - b.x, a.y - b.y, a.z - b.z}; }
+__device__ __forceinline__ f3 mul(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
+__device__ __forceinline__ f3 scale(f3 a, float s) { return {a.x * s, a.y * s, a.z * s}; }
+__device__ __forceinline__ f3 sscale(float s, f3 a) { return {s * a.x, s * a.y, s * a.z}; }
+__device__ __forceinline__ f3 divs(f3 a, float s) { return {a.x / s, a.y / s, a.z / s}; }
+__device__ __forceinline__ f3 neg(f3 a) { return {-a.x, -a.y, -a.z}; }
+__device__ __forceinline__ float dot(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ float len(f3 a) { return __builtin_sqrtf(dot(a, a)); }
+__device__ __forceinline__ f3 cross(f3 a, f3 b) {
+    return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
+}
+__device__ __forceinline__ f3 xyz(float4 v) { return {v.x, v.y, v.z}; }
+__device__ __forceinline__ f3 xyz(q4 v) { return {v.x, v.y, v.z}; }
+__device__ __forceinline__ q4 toq(float4 v) { return {v.x, v.y, v.z, v.w}; }
+__device__ __forceinline__ float4 tof4(q4 v) { return make_float4(v.x, v.y, v.z, v.w); }
+__device__ __forceinline__ float4 tof4(f3 v, float w) { return make_float4(v.x, v.y, v.z, w); }
+
+__device__ __forceinline__ q4 qadd(q4 a, q4 b) { return {a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w}; }
+__device__ __forceinline__ q4 qsub(q4 a, q4 b) { return {a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w}; }
+__device__ __forceinline__ q4 qscale(q4 a, float s) { return {a.x * s, a.y * s, a.z * s, a.w * s}; }
+__device__ __forceinline__ q4 qneg(q4 a) { return {-a.x, -a.y, -a.z, -a.w}; }
+__device__ __forceinline__ q4 qconj(q4 q) { return {-q.x, -q.y, -q.z, q.w}; }
+// Hamilton product, xyzw storage.
+__device__ __forceinline__ q4 qmul(q4 a, q4 b) {
+    return {a.w * b.x + a.x * b.w + a.y * b.z - a.z * b.y,
+            a.w * b.y - a.x * b.z + a.y * b.w + a.z * b.x,
+            a.w * b.z + a.x * b.y - a.y * b.x + a.z * b.w,
+            a.w * b.w - a.x * b.x - a.y * b.y - a.z * b.z};
+}
+// v + 2 (w (q x v) + q x (q x v))
+__device__ __forceinline__ f3 qrot(f3 v, q4 q) {
+    f3 qv = {q.x, q.y, q.z};
+    f3 uv = cross(qv, v);
+    f3 uuv = cross(qv, uv);
+    return {v.x + 2.0f * (q.w * uv.x + uuv.x), v.y + 2.0f * (q.w * uv.y + uuv.y),
+            v.z + 2.0f * (q.w * uv.z + uuv.z)};
+}
+__device__ __forceinline__ float qlen(q4 q) { return __builtin_sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w); }
+__device__ __forceinline__ q4 qnormalize(q4 q) {
+    float l = qlen(q);
+    return l > 1e-8f ? q4{q.x / l, q.y / l, q.z / l, q.w / l} : q4{0.0f, 0.0f, 0.0f, 1.0f};
+}
+// Quaternion step q + s * ((d, 0) (x) q) used by every XPBD rotation update.
+__device__ __forceinline__ q4 qdelta(f3 d, q4 q) { return qscale(qmul(mk4(d.x, d.y, d.z, 0.0f), q), 0.5f); }
+__device__ __forceinline__ float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+
+// atan2 / asin after S. Moshier's Cephes single-precision routines (atanf.c, asinf.c):
+// reduction at tan(3pi/8) and tan(pi/8) with a degree-9 odd polynomial for atan; the 0.5
+// split with sqrt reduction and a degree-11 odd polynomial for asin. Max error 3 ulp.
+constexpr float kPi = 3.14159265358979323846f;
+constexpr float kPiO2 = 1.57079632679489661923f;
+constexpr float kPiO4 = 0.78539816339744830962f;
+
+__device__ __forceinline__ float atan_nonneg(float x) {
+    float y0, t;
+    if (x > 2.414213562373095f) { y0 = kPiO2; t = -1.0f / x; }
+    else if (x > 0.4142135623730950f) { y0 = kPiO4; t = (x - 1.0f) / (x + 1.0f); }
+    else { y0 = 0.0f; t = x; }
+    float z = t * t;
+    float p = (((8.05374449538e-2f * z - 1.38776856032e-1f) * z + 1.99777106478e-1f) * z - 3.33329491539e-1f) * z * t + t;
+    return y0 + p;
+}
+
+__device__ __forceinline__ float z_atan2f(float y, float x) {
+    if (__builtin_isnan(x) || __builtin_isnan(y)) return x + y;
+    if (x == 0.0f) {
+        if (y > 0.0f) return kPiO2;
+        if (y < 0.0f) return -kPiO2;
+        return __builtin_signbit(x) ? (__builtin_signbit(y) ? -kPi : kPi) : y;
+    }
+    if (y == 0.0f) return __builtin_signbit(x) ? (__builtin_signbit(y) ? -kPi : kPi) : y;
+    float ax = __builtin_fabsf(x), ay = __builtin_fabsf(y);
+    float r;
+    if (__builtin_isinf(ax)) {
+        if (__builtin_isinf(ay)) r = x > 0.0f ? kPiO4 : 3.0f * kPiO4;
+        else r = x > 0.0f ? 0.0f : kPi;
+    } else if (__builtin_isinf(ay)) {
+        r = kPiO2;
+    } else {
+        float a = atan_nonneg(ay / ax);
+        r = x > 0.0f ? a : kPi - a;
+    }
+    return y < 0.0f ? -r : r;
+}
+
+__device__ __forceinline__ float z_asinf(float x) {
+    if (__builtin_isnan(x)) return x;
+    float a = __builtin_fabsf(x);
+    if (a > 1.0f) return __builtin_nanf("");
+    float z, t;
+    bool flag = a > 0.5f;
+    if (flag) { z = 0.5f * (1.0f - a); t = __builtin_sqrtf(z); }
+    else { t = a; z = a * a; }
+    float p = ((((4.2163199048e-2f * z + 2.4181311049e-2f) * z + 4.5470025998e-2f) * z + 7.4953002686e-2f) * z + 1.6666752422e-1f) * z * t + t;
+    if (flag) p = kPiO2 - (p + p);
+    return x < 0.0f ? -p : p;
+}
+
+}  // namespace za

@@ -1,0 +1,824 @@
+// Fused physics step for CDNA4 (gfx950).
+//
+// One single-wave workgroup steps EPW environments; each environment owns G = 64 / EPW
+// lanes and an LDS working set (bodies, joint state, lambdas, the contact list and the
+// previous-contact snapshot). A launch runs every substep of one zeno_world_step call, so
+// HBM is read once and written once per call while all solver iterations stay in LDS.
+//
+// Stage order and arithmetic follow World.stepOnce (src/world/world.zig:934-1293) and the
+// MSL kernels of src/shaders/all_shaders.metal, cited per stage. Where the reference runs
+// unordered atomics or races, this kernel produces the deterministic schedule:
+//   S1 broad-phase appends in (g, g') order: wave ballot + popcount prefix per env;
+//   S2 per-body joint-force sums in ascending joint order, body_a before body_b;
+//   S3 joint constraints per colour (bodies in one colour are disjoint);
+//   S4 contact slots Gauss-Seidel in slot order: slots are levelled so that a slot runs
+//      after every earlier slot sharing a body it writes, then levels run in order.
+// The stable contact sort (all_shaders.metal:711-745) is a rank sort over a logical->physical
+// permutation, so 64-byte records never move in LDS; the permutation is applied when the
+// list is written back.
+#include <hip/hip_runtime.h>
+
+#include "dmath.h"
+#include "step.h"
+
+namespace za {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kMaxRecsPerLane = 8;
+
+__device__ __forceinline__ uint32_t pair_key(uint32_t a, uint32_t b) {
+    uint32_t lo = a < b ? a : b, hi = a < b ? b : a;
+    return (lo << 16) | hi;
+}
+
+struct Lds {
+    float4 *pos, *quat, *vel, *angvel, *ppos, *pquat, *frc, *trq, *vb;
+    float *jt, *jp, *jv, *lam;
+    ContactRec* con;
+    uint16_t* perm;
+    uint32_t* skey;
+    uint32_t* pkey;
+    float4 *ppen, *pimp;
+    uint16_t *order, *loff, *last;
+    uint32_t* misc;
+};
+
+__device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
+    Lds s;
+    s.pos = (float4*)(base + L.pos); s.quat = (float4*)(base + L.quat);
+    s.vel = (float4*)(base + L.vel); s.angvel = (float4*)(base + L.angvel);
+    s.ppos = (float4*)(base + L.ppos); s.pquat = (float4*)(base + L.pquat);
+    s.frc = (float4*)(base + L.frc); s.trq = (float4*)(base + L.trq);
+    s.vb = (float4*)(base + L.vbefore);
+    s.jt = (float*)(base + L.jt); s.jp = (float*)(base + L.jp); s.jv = (float*)(base + L.jv);
+    s.lam = (float*)(base + L.lam);
+    s.con = (ContactRec*)(base + L.con);
+    s.perm = (uint16_t*)(base + L.perm);
+    s.skey = (uint32_t*)(base + L.skey);
+    s.pkey = (uint32_t*)(base + L.pkey);
+    s.ppen = (float4*)(base + L.ppen); s.pimp = (float4*)(base + L.pimp);
+    s.order = (uint16_t*)(base + L.order); s.loff = (uint16_t*)(base + L.loff);
+    s.last = (uint16_t*)(base + L.last);
+    s.misc = (uint32_t*)(base + L.misc);
+    return s;
+}
+
+__device__ __forceinline__ void set_xyz(float4* p, f3 v) { p->x = v.x; p->y = v.y; p->z = v.z; }
+
+// ---------------------------------------------------------------------------------------
+// solve_joints, all_shaders.metal:909-1399, one constraint against LDS body state.
+// ---------------------------------------------------------------------------------------
+__device__ void solve_constraint(const StepArgs& a, const Lds& s, uint32_t ci) {
+    const ConstraintRec& c = a.tmpl[ci];
+    const uint32_t type = c.indices[3] & 0xFFu;
+    if (type > 10) return;
+    const uint32_t ia = c.indices[0], ib = c.indices[1];
+    const float4 imi_a = a.invmi[ia], imi_b = a.invmi[ib];
+    const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
+    const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
+    if (inv_mass_a + inv_mass_b < 1e-8f) return;
+    float4* Pa = &s.pos[ia];
+    float4* Pb = &s.pos[ib];
+    float4* Qa = &s.quat[ia];
+    float4* Qb = &s.quat[ib];
+    const f3 pos_a = xyz(*Pa), pos_b = xyz(*Pb);
+    const q4 quat_a = toq(*Qa), quat_b = toq(*Qb);
+    const float dt = a.dt;
+    const float alpha_tilde = c.anchor_a[3] / (dt * dt);
+
+    if (type == C_POSITIONAL) {
+        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
+        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
+        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
+        float C = len(diff);
+        if (C > 1e-6f) {
+            f3 n = divs(diff, C);
+            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
+            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+            float lambda_prev = s.lam[ci];
+            float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
+            s.lam[ci] = lambda_prev + d_lambda;
+            f3 impulse = sscale(d_lambda, n);
+            f3 rc_a = sub(r_a, qrot(xyz(a.com[ia]), quat_a));
+            f3 rc_b = sub(r_b, qrot(xyz(a.com[ib]), quat_b));
+            if (inv_mass_a > 0) {
+                set_xyz(Pa, add(xyz(*Pa), scale(impulse, inv_mass_a)));
+                *Qa = tof4(qnormalize(qadd(quat_a, qdelta(mul(cross(rc_a, impulse), iI_a), quat_a))));
+            }
+            if (inv_mass_b > 0) {
+                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
+                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(rc_b, impulse), iI_b), quat_b))));
+            }
+        }
+    } else if (type == C_WELD) {
+        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
+        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
+        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
+        float C = len(diff);
+        if (C > 1e-6f) {
+            f3 n = divs(diff, C);
+            f3 rn_b = cross(r_b, n);
+            float w_b = inv_mass_b + dot(mul(rn_b, iI_b), rn_b);
+            if (w_b > 1e-8f) {
+                float d_lambda = (-C) / (w_b + alpha_tilde);
+                f3 impulse = sscale(d_lambda, n);
+                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
+                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b))));
+            }
+        }
+        q4 target = mk4(c.axis_target[0], c.axis_target[1], c.axis_target[2], c.axis_target[3]);
+        q4 qa = toq(*Qa), qb = toq(*Qb);
+        q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
+        if (q_err.w < 0) q_err = qneg(q_err);
+        f3 e = xyz(q_err);
+        float sh = len(e);
+        if (sh > 1e-6f) {
+            f3 axis_rel = divs(e, sh);
+            float angle = 2.0f * z_atan2f(sh, q_err.w);
+            f3 aw = qrot(axis_rel, qa);
+            float w_b = dot(mul(aw, iI_b), aw);
+            if (w_b > 1e-8f) {
+                float d_lambda_ang = angle / (w_b + alpha_tilde);
+                f3 ang_impulse = sscale(d_lambda_ang, aw);
+                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
+            }
+        }
+    } else if (type == C_ANGULAR) {
+        q4 qa = toq(*Qa), qb = toq(*Qb);
+        f3 axa = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), qa);
+        f3 axb = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), qb);
+        f3 cr = cross(axa, axb);
+        float sin_angle = len(cr);
+        if (sin_angle > 1e-6f) {
+            f3 n = divs(cr, sin_angle);
+            float ang_C = z_asinf(clampf(sin_angle, -1.0f, 1.0f));
+            float w = dot(mul(n, iI_a), n) + dot(mul(n, iI_b), n);
+            if (w > 1e-8f) {
+                float d_lambda = -ang_C / (w + alpha_tilde);
+                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(sscale(d_lambda, n), iI_a), qa))));
+                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qadd(qb, qdelta(mul(sscale(-d_lambda, n), iI_b), qb))));
+            }
+        }
+    } else if (type == C_ANGULAR_LIMIT) {
+        f3 axis_local = mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]);
+        float lower = c.limits[0], upper = c.limits[1];
+        q4 qa = toq(*Qa), qb = toq(*Qb);
+        q4 q_rel = qmul(qconj(qa), qb);
+        float angle = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
+        float violation = 0.0f;
+        if (angle < lower) violation = lower - angle;
+        else if (angle > upper) violation = upper - angle;
+        if (__builtin_fabsf(violation) > 1e-6f) {
+            f3 aw = qrot(axis_local, qa);
+            float w = dot(mul(aw, iI_a), aw) + dot(mul(aw, iI_b), aw);
+            if (w > 1e-8f) {
+                float d_lambda = violation / (w + alpha_tilde);
+                f3 ang_impulse = sscale(d_lambda, aw);
+                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(ang_impulse, iI_a), qa))));
+                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
+            }
+        }
+    } else if (type == C_LINEAR_LIMIT) {
+        f3 axis_local = mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]);
+        float lower = c.limits[0], upper = c.limits[1];
+        q4 qa = toq(*Qa), qb = toq(*Qb);
+        f3 r_a = qrot(mk3(0.0f, 0.0f, 0.0f), qa);
+        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), qb);
+        f3 aw = qrot(axis_local, qa);
+        float dist = dot(sub(add(pos_b, r_b), add(pos_a, r_a)), aw);
+        float violation = 0.0f;
+        if (dist < lower) violation = lower - dist;
+        else if (dist > upper) violation = upper - dist;
+        if (__builtin_fabsf(violation) > 1e-6f) {
+            f3 n = violation > 0 ? aw : neg(aw);
+            float abs_v = __builtin_fabsf(violation);
+            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
+            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+            if (w > 1e-8f) {
+                float d_lambda = abs_v / (w + alpha_tilde);
+                f3 impulse = sscale(d_lambda, n);
+                if (inv_mass_a > 0) set_xyz(Pa, sub(xyz(*Pa), scale(impulse, inv_mass_a)));
+                if (inv_mass_b > 0) set_xyz(Pb, add(xyz(*Pb), scale(impulse, inv_mass_b)));
+            }
+        }
+    } else if (type == C_SLIDER) {
+        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
+        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
+        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
+        f3 aw = qrot(mk3(c.axis_target[0], c.axis_target[1], c.axis_target[2]), quat_a);
+        float along = dot(diff, aw);
+        f3 perp = sub(diff, sscale(along, aw));
+        float perp_len = len(perp);
+        if (perp_len > 1e-6f) {
+            f3 n = divs(perp, perp_len);
+            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
+            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+            float d_lambda = (-perp_len) / (w + alpha_tilde);
+            f3 impulse = sscale(d_lambda, n);
+            if (inv_mass_a > 0) {
+                set_xyz(Pa, add(xyz(*Pa), scale(impulse, inv_mass_a)));
+                *Qa = tof4(qnormalize(qadd(quat_a, qdelta(mul(cross(r_a, impulse), iI_a), quat_a))));
+            }
+            if (inv_mass_b > 0) {
+                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
+                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b))));
+            }
+        }
+        q4 target = mk4(c.limits[0], c.limits[1], c.limits[2], c.limits[3]);
+        q4 qa = toq(*Qa), qb = toq(*Qb);
+        q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
+        if (q_err.w < 0) q_err = qneg(q_err);
+        f3 e = xyz(q_err);
+        float sh = len(e);
+        if (sh > 1e-6f) {
+            f3 axis_err = divs(e, sh);
+            float angle_err = 2.0f * z_atan2f(sh, q_err.w);
+            f3 aw2 = qrot(axis_err, qa);
+            float w = dot(mul(aw2, iI_a), aw2) + dot(mul(aw2, iI_b), aw2);
+            if (w > 1e-8f) {
+                float d_lambda_ang = angle_err / (w + alpha_tilde);
+                f3 ang_impulse = sscale(d_lambda_ang, aw2);
+                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(ang_impulse, iI_a), qa))));
+                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// solve_contacts, all_shaders.metal:1644-1793, one contact record.
+// ---------------------------------------------------------------------------------------
+__device__ void solve_contact(const StepArgs& a, const Lds& s, ContactRec* cr) {
+    const float4 pp = *(const float4*)cr->position_pen;
+    if (pp.w < 0) return;
+    const float4 nf = *(const float4*)cr->normal_friction;
+    const uint32_t ia = cr->indices[0], ib = cr->indices[1];
+    const float4 imi_a = a.invmi[ia], imi_b = a.invmi[ib];
+    const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
+    const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
+    const float inv_mass_sum = inv_mass_a + inv_mass_b;
+    if (inv_mass_sum < 1e-8f) return;
+    const f3 normal = mk3(nf.x, nf.y, nf.z);
+    const float penetration = pp.w, friction = nf.w;
+    const f3 cp = mk3(pp.x, pp.y, pp.z);
+    float4* Pa = &s.pos[ia];
+    float4* Pb = &s.pos[ib];
+    float4* Va = &s.vel[ia];
+    float4* Vb = &s.vel[ib];
+    float4* Wa = &s.angvel[ia];
+    float4* Wb = &s.angvel[ib];
+    const f3 r_a = sub(cp, xyz(*Pa)), r_b = sub(cp, xyz(*Pb));
+    const f3 vel_a = add(xyz(*Va), cross(xyz(*Wa), r_a));
+    const f3 vel_b = add(xyz(*Vb), cross(xyz(*Wb), r_b));
+    const f3 rel_vel = sub(vel_a, vel_b);
+    const float vel_normal = dot(rel_vel, normal);
+    const f3 vel_tangent = sub(rel_vel, sscale(vel_normal, normal));
+    const float tangent_speed = len(vel_tangent);
+    const f3 rn_a = cross(r_a, normal), rn_b = cross(r_b, normal);
+    const float w_normal = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+    if (w_normal < 1e-8f) return;
+    const float bias = a.baumgarte * fmaxf(penetration - a.slop, 0.0f) / a.dt;
+    const float restitution = cr->impulses[3];
+    const float vel_restitution = vel_normal < -0.5f ? restitution * vel_normal : 0.0f;
+    float j_n = (-(vel_normal + vel_restitution) + bias) / w_normal;
+    j_n = fmaxf(j_n, 0.0f);
+    const f3 impulse_n = sscale(j_n, normal);
+    const float pos_correction = a.baumgarte * fmaxf(penetration - a.slop, 0.0f);
+    if (inv_mass_a > 1e-8f) {
+        set_xyz(Va, add(xyz(*Va), scale(impulse_n, inv_mass_a)));
+        set_xyz(Wa, add(xyz(*Wa), mul(cross(r_a, impulse_n), iI_a)));
+        float ratio = inv_mass_a / inv_mass_sum;
+        set_xyz(Pa, add(xyz(*Pa), sscale(pos_correction * ratio, normal)));
+    }
+    if (inv_mass_b > 1e-8f) {
+        set_xyz(Vb, sub(xyz(*Vb), scale(impulse_n, inv_mass_b)));
+        set_xyz(Wb, sub(xyz(*Wb), mul(cross(r_b, impulse_n), iI_b)));
+        float ratio = inv_mass_b / inv_mass_sum;
+        set_xyz(Pb, sub(xyz(*Pb), sscale(pos_correction * ratio, normal)));
+    }
+    const float j_n_acc = cr->impulses[0] + j_n;
+    if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
+        f3 tangent = divs(vel_tangent, tangent_speed);
+        f3 rt_a = cross(r_a, tangent), rt_b = cross(r_b, tangent);
+        float w_tangent = (inv_mass_a + dot(mul(rt_a, iI_a), rt_a)) + (inv_mass_b + dot(mul(rt_b, iI_b), rt_b));
+        if (w_tangent > 1e-8f) {
+            float j_t = fminf(tangent_speed / w_tangent, friction * j_n_acc);
+            f3 impulse_t = sscale(j_t, tangent);
+            if (inv_mass_a > 1e-8f) {
+                set_xyz(Va, sub(xyz(*Va), scale(impulse_t, inv_mass_a)));
+                set_xyz(Wa, sub(xyz(*Wa), mul(cross(r_a, impulse_t), iI_a)));
+            }
+            if (inv_mass_b > 1e-8f) {
+                set_xyz(Vb, add(xyz(*Vb), scale(impulse_t, inv_mass_b)));
+                set_xyz(Wb, add(xyz(*Wb), mul(cross(r_b, impulse_t), iI_b)));
+            }
+        }
+    }
+    cr->impulses[0] = j_n;
+}
+
+// ---------------------------------------------------------------------------------------
+// narrow_phase, all_shaders.metal:751-894, one slot.
+// ---------------------------------------------------------------------------------------
+__device__ void narrow_slot(const StepArgs& a, const Lds& s, ContactRec* c) {
+    const uint32_t body_a = c->indices[0], body_b = c->indices[1];
+    const GeomRec& ga = a.geoms[c->indices[2]];
+    const GeomRec& gb = a.geoms[c->indices[3]];
+    const f3 pos_a = add(xyz(s.pos[body_a]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
+    const f3 pos_b = add(xyz(s.pos[body_b]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
+    const uint32_t type_a = ga.type_body[0], type_b = gb.type_body[0];
+    f3 normal = mk3(0, 0, 0), cp = mk3(0, 0, 0);
+    float pen = 0.0f;
+    bool hit = false;
+    if (type_a == GEOM_SPHERE && type_b == GEOM_SPHERE) {
+        float ra = ga.pos_size0[3], rb = gb.pos_size0[3];
+        f3 diff = sub(pos_b, pos_a);
+        float dist = len(diff);
+        float min_dist = ra + rb;
+        if (dist < min_dist && dist > 1e-6f) {
+            normal = divs(diff, dist);
+            pen = min_dist - dist;
+            cp = add(pos_a, scale(normal, ra - pen * 0.5f));
+            hit = true;
+        }
+    } else if ((type_a == GEOM_SPHERE && type_b == GEOM_PLANE) || (type_a == GEOM_PLANE && type_b == GEOM_SPHERE)) {
+        const f3 plane_normal = mk3(0, 0, 1);
+        f3 sphere_pos = type_a == GEOM_SPHERE ? pos_a : pos_b;
+        float radius = type_a == GEOM_SPHERE ? ga.pos_size0[3] : gb.pos_size0[3];
+        f3 plane_pos = type_a == GEOM_SPHERE ? pos_b : pos_a;
+        float signed_dist = dot(sub(sphere_pos, plane_pos), plane_normal);
+        if (signed_dist < radius) {
+            normal = plane_normal;
+            pen = radius - signed_dist;
+            cp = sub(sphere_pos, scale(plane_normal, signed_dist + pen * 0.5f));
+            hit = true;
+            if (type_a == GEOM_PLANE) normal = neg(normal);
+        }
+    } else if ((type_a == GEOM_CAPSULE && type_b == GEOM_PLANE) || (type_a == GEOM_PLANE && type_b == GEOM_CAPSULE)) {
+        const f3 plane_normal = mk3(0, 0, 1);
+        const GeomRec& gc = type_a == GEOM_CAPSULE ? ga : gb;
+        f3 cap_pos = type_a == GEOM_CAPSULE ? pos_a : pos_b;
+        float r = gc.pos_size0[3], hl = gc.params[0];
+        f3 axis = qrot(mk3(0, 0, 1), mk4(gc.quat[0], gc.quat[1], gc.quat[2], gc.quat[3]));
+        f3 p1 = sub(cap_pos, scale(axis, hl));
+        f3 p2 = add(cap_pos, scale(axis, hl));
+        float d1 = p1.z - r, d2 = p2.z - r;
+        if (d1 < 0 || d2 < 0) {
+            f3 deepest = d1 < d2 ? p1 : p2;
+            float dist = fminf(d1, d2);
+            normal = type_a == GEOM_CAPSULE ? plane_normal : neg(plane_normal);
+            pen = -dist;
+            cp = deepest;
+            cp.z = 0;
+            hit = true;
+        }
+    }
+    if (hit) {
+        float mu = __builtin_sqrtf(ga.params[2] * gb.params[2]);
+        *(float4*)c->position_pen = make_float4(cp.x, cp.y, cp.z, pen);
+        *(float4*)c->normal_friction = make_float4(normal.x, normal.y, normal.z, mu);
+        *(float4*)c->impulses = make_float4(0.0f, 0.0f, 0.0f, a.restitution);
+    } else {
+        c->position_pen[3] = -1.0f;
+    }
+}
+
+template <int EPW>
+__global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
+    constexpr int G = kWave / EPW;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int le = tid / G;
+    const int sl = tid % G;
+    const uint32_t env = blockIdx.x * EPW + le;
+    const bool live = env < a.E;
+    const Lds s = bind_lds(smem + le * a.lds.bytes, a.lds);
+    const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
+    const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
+
+    // ---- Load the env's working set (HBM -> LDS) --------------------------------------
+    uint32_t count = 0, pcount = 0;
+    bool detached = false;
+    if (live) {
+        const size_t eb = (size_t)env * B;
+        for (uint32_t b = sl; b < B; b += G) {
+            s.pos[b] = a.pos[eb + b];
+            s.quat[b] = a.quat[eb + b];
+            float4 v = a.vel[eb + b];
+            s.vel[b] = v;
+            s.vb[b] = v;
+            s.angvel[b] = a.angvel[eb + b];
+        }
+        for (uint32_t j = sl; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
+        for (uint32_t i = sl; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
+        const ContactRec* gc = a.contacts + (size_t)env * M;
+        for (uint32_t k = sl; k < M; k += G) {
+            const float4* src = (const float4*)&gc[k];
+            float4* dst = (float4*)&s.con[k];
+            dst[0] = src[0]; dst[1] = src[1]; dst[2] = src[2]; dst[3] = src[3];
+            s.perm[k] = (uint16_t)k;
+        }
+        count = a.counts[env];
+        pcount = a.pcounts[env];
+        detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
+    }
+    __syncthreads();
+
+    for (uint32_t step = 0; step < a.substeps; ++step) {
+        // ---- Previous-contact snapshot (cache_contacts of the last substep) -----------
+        if (live) {
+            const uint32_t pn = pcount < M ? pcount : M;
+            const bool from_det = step == 0 && detached;
+            for (uint32_t k = sl; k < pn; k += G) {
+                const ContactRec* r = from_det ? &a.prev_contacts[(size_t)env * M + k] : &s.con[s.perm[k]];
+                s.pkey[k] = pair_key(r->indices[0], r->indices[1]);
+                s.ppen[k] = *(const float4*)r->position_pen;
+                s.pimp[k] = *(const float4*)r->impulses;
+            }
+        }
+        // ---- A: warm_start_constraints + apply_actions (:1408-1426, :196-229) ---------
+        if (live) {
+            for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
+            for (uint32_t k = sl; k < a.A; k += G) {
+                const ActuatorRec& act = a.acts[k];
+                float ctrl = clampf(a.actions[(size_t)env * a.A + k], act.params[1], act.params[2]);
+                float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
+                s.jt[(uint32_t)act.params[0]] = torque;
+            }
+        }
+        __syncthreads();
+        // ---- B: compute_forces + update_kinematic (:345-388, :304-339) ----------------
+        if (live) {
+            for (uint32_t b = sl; b < B; b += G) {
+                const float4 imi = a.invmi[b];
+                if (a.kinematic[b]) {
+                    f3 p = add(xyz(s.pos[b]), scale(xyz(s.vel[b]), a.dt));
+                    s.pos[b] = tof4(p, 0.0f);
+                    q4 q = toq(s.quat[b]);
+                    f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
+                    s.quat[b] = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
+                }
+                if (imi.x < 1e-8f) {
+                    s.frc[b] = make_float4(0, 0, 0, 0);
+                    s.trq[b] = make_float4(0, 0, 0, 0);
+                } else {
+                    float mass = 1.0f / imi.x;
+                    f3 force = mk3(a.gx * mass, a.gy * mass, a.gz * mass);
+                    s.frc[b] = tof4(force, 0.0f);
+                    f3 cw = qrot(xyz(a.com[b]), toq(s.quat[b]));
+                    s.trq[b] = tof4(cross(cw, force), 0.0f);
+                }
+            }
+        }
+        __syncthreads();
+        // ---- C: apply_joint_forces (S2) + save_prev_state (:122-190, :1900-1913) ------
+        if (live) {
+            for (uint32_t b = sl; b < B; b += G) {
+                if (b > 0) {
+                    float4 f = s.frc[b], t = s.trq[b];
+                    for (uint32_t j = 0; j < a.J; ++j) {
+                        const JointRec& jr = a.joints[j];
+                        const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
+                        if (ja != b && jb != b) continue;
+                        const float tau = s.jt[j];
+                        if (__builtin_fabsf(tau) < 1e-6f) continue;
+                        f3 w = scale(qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), toq(s.quat[ja])), tau);
+                        f3 d = ja == b ? neg(w) : w;
+                        if ((uint32_t)jr.params[0] == JOINT_PRISMATIC) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
+                        else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
+                    }
+                    s.frc[b] = f;
+                    s.trq[b] = t;
+                }
+                s.ppos[b] = s.pos[b];
+                s.pquat[b] = s.quat[b];
+            }
+        }
+        __syncthreads();
+        // ---- D: integrate (:394-462) -------------------------------------------------
+        if (live) {
+            for (uint32_t b = sl; b < B; b += G) {
+                const float4 imi = a.invmi[b];
+                if (imi.x < 1e-8f) continue;
+                f3 vel = add(xyz(s.vel[b]), scale(scale(xyz(s.frc[b]), imi.x), a.dt));
+                vel = scale(vel, 0.999f);
+                f3 pos = add(xyz(s.pos[b]), scale(vel, a.dt));
+                s.vel[b] = tof4(vel, 0.0f);
+                s.pos[b] = tof4(pos, 0.0f);
+                f3 om = add(xyz(s.angvel[b]), scale(mul(mk3(imi.y, imi.z, imi.w), xyz(s.trq[b])), a.dt));
+                om = scale(om, 0.999f);
+                q4 q = toq(s.quat[b]);
+                f3 h = scale(scale(om, a.dt), 0.5f);
+                q = qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q));
+                float ql = qlen(q);
+                q = ql > 1e-8f ? q4{q.x / ql, q.y / ql, q.z / ql, q.w / ql} : q4{0.0f, 0.0f, 0.0f, 1.0f};
+                s.angvel[b] = tof4(om, 0.0f);
+                s.quat[b] = tof4(q);
+            }
+        }
+        __syncthreads();
+        // ---- E: broad_phase (S1), :468-533 -------------------------------------------
+        const uint32_t count_before = count;
+        {
+            const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
+            const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
+            for (uint32_t base = 0; base < a.P; base += G) {
+                const uint32_t p = base + sl;
+                bool hit = false;
+                uint32_t g = 0, h = 0, ba = 0, bb = 0;
+                if (live && p < a.P) {
+                    const uint32_t pr = a.pairs[p];
+                    g = pr & 0xFFFFu;
+                    h = pr >> 16;
+                    const GeomRec& ga = a.geoms[g];
+                    const GeomRec& gb = a.geoms[h];
+                    ba = ga.type_body[1];
+                    bb = gb.type_body[1];
+                    if (ga.type_body[0] == GEOM_PLANE || gb.type_body[0] == GEOM_PLANE) {
+                        hit = true;
+                    } else {
+                        f3 pa = add(xyz(s.pos[ba]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
+                        f3 pb = add(xyz(s.pos[bb]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
+                        f3 diff = sub(pb, pa);
+                        float min_dist = ga.pos_size0[3] + gb.pos_size0[3] + 0.1f;
+                        hit = !(dot(diff, diff) >= min_dist * min_dist);  // NaN distances pass, as in :521
+                    }
+                }
+                const uint64_t ballot = __ballot(hit);
+                const uint32_t rank = (uint32_t)__popcll(ballot & below);
+                const uint32_t total = (uint32_t)__popcll(ballot & group_mask);
+                if (hit) {
+                    const uint32_t slot = count + rank;
+                    if (slot < M) {
+                        uint32_t* idx = s.con[s.perm[slot]].indices;
+                        idx[0] = ba; idx[1] = bb; idx[2] = g; idx[3] = h;
+                    }
+                }
+                count += total;
+            }
+        }
+        __syncthreads();
+        // ---- E.5: sort_contacts (:711-745), stable rank sort over the permutation ------
+        {
+            const uint32_t n = count < M ? count : M;
+            const bool need = live && count_before < M && count > count_before && n > 1;
+            if (need) {
+                for (uint32_t k = sl; k < n; k += G) {
+                    const uint32_t* idx = s.con[s.perm[k]].indices;
+                    s.skey[k] = pair_key(idx[0], idx[1]);
+                }
+            }
+            __syncthreads();
+            uint16_t keep[kMaxRecsPerLane];
+            uint32_t dst[kMaxRecsPerLane];
+            if (need) {
+#pragma unroll
+                for (int r = 0; r < kMaxRecsPerLane; ++r) {
+                    const uint32_t k = sl + r * G;
+                    if (k < n) {
+                        const uint32_t key = s.skey[k];
+                        uint32_t rank = 0;
+                        for (uint32_t j = 0; j < n; ++j) {
+                            const uint32_t kj = s.skey[j];
+                            rank += (kj < key || (kj == key && j < k)) ? 1u : 0u;
+                        }
+                        keep[r] = s.perm[k];
+                        dst[r] = rank;
+                    }
+                }
+            }
+            __syncthreads();
+            if (need) {
+#pragma unroll
+                for (int r = 0; r < kMaxRecsPerLane; ++r) {
+                    const uint32_t k = sl + r * G;
+                    if (k < n) s.perm[dst[r]] = keep[r];
+                }
+            }
+        }
+        __syncthreads();
+        // ---- F: narrow_phase (:751-894) -----------------------------------------------
+        const uint32_t n_live = count < M ? count : M;
+        if (live) {
+            for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, s, &s.con[s.perm[k]]);
+        }
+        __syncthreads();
+        // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
+        // The snapshot is key-sorted (it is a sorted list from the last substep), so the
+        // entries with this slot's body pair form one run found by binary search; scanning
+        // that run in index order gives the reference's first strict minimum.
+        if (live) {
+            const uint32_t pn = pcount < M ? pcount : M;
+            for (uint32_t k = sl; k < n_live; k += G) {
+                ContactRec* c = &s.con[s.perm[k]];
+                if (c->position_pen[3] < 0) continue;
+                const uint32_t key = pair_key(c->indices[0], c->indices[1]);
+                uint32_t lo = 0, hi = pn;
+                while (lo < hi) {
+                    uint32_t mid = (lo + hi) >> 1;
+                    if (s.pkey[mid] < key) lo = mid + 1; else hi = mid;
+                }
+                const f3 p = mk3(c->position_pen[0], c->position_pen[1], c->position_pen[2]);
+                float best = 0.04f;
+                int best_i = -1;
+                for (uint32_t i = lo; i < pn && s.pkey[i] == key; ++i) {
+                    const float4 q = s.ppen[i];
+                    if (q.w < 0) continue;
+                    f3 d = sub(mk3(q.x, q.y, q.z), p);
+                    float dsq = dot(d, d);
+                    if (dsq < best) { best = dsq; best_i = (int)i; }
+                }
+                if (best_i >= 0) {
+                    const float4 im = s.pimp[best_i];
+                    c->impulses[0] = im.x * 0.8f;
+                    c->impulses[1] = im.y * 0.8f;
+                    c->impulses[2] = im.z * 0.8f;
+                }
+            }
+        }
+        // ---- Contact levels for S4 (one lane per env) --------------------------------
+        if (live && sl == 0) {
+            for (uint32_t b = 0; b < B; ++b) s.last[b] = 0;
+            uint32_t nlev = 0;
+            for (uint32_t k = 0; k < n_live; ++k) {
+                const ContactRec* c = &s.con[s.perm[k]];
+                uint32_t lv = 0;
+                if (!(c->position_pen[3] < 0)) {  // solve_contacts skips only pen < 0 (:1667)
+                    const uint32_t ia = c->indices[0], ib = c->indices[1];
+                    const bool da = a.invmi[ia].x > 1e-8f, db = a.invmi[ib].x > 1e-8f;
+                    uint32_t l0 = 0;
+                    if (da) l0 = s.last[ia];
+                    if (db && s.last[ib] > l0) l0 = s.last[ib];
+                    lv = l0 + 1;
+                    if (da) s.last[ia] = (uint16_t)lv;
+                    if (db) s.last[ib] = (uint16_t)lv;
+                    if (lv > nlev) nlev = lv;
+                }
+                s.skey[k] = lv;
+            }
+            // Counting sort of live slots by level: order[loff[L-1] .. loff[L]) = level L.
+            for (uint32_t l = 0; l <= nlev; ++l) s.loff[l] = 0;
+            for (uint32_t k = 0; k < n_live; ++k) if (s.skey[k]) s.loff[s.skey[k]]++;
+            uint32_t run = 0;
+            for (uint32_t l = 0; l <= nlev; ++l) { uint32_t c = s.loff[l]; s.loff[l] = (uint16_t)run; run += c; }
+            for (uint32_t k = 0; k < n_live; ++k) {
+                uint32_t lv = s.skey[k];
+                if (lv) s.order[s.loff[lv]++] = (uint16_t)k;
+            }
+            // loff[l] now holds the end of level l; shift so that level L spans [loff[L-1], loff[L]).
+            s.misc[2] = nlev;
+        }
+        __syncthreads();
+        uint32_t max_lev = 0;
+        for (int e2 = 0; e2 < EPW; ++e2) {
+            const uint32_t* m2 = (const uint32_t*)(smem + e2 * a.lds.bytes + a.lds.misc);
+            if (blockIdx.x * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
+        }
+        const uint32_t my_lev = live ? s.misc[2] : 0;
+        // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
+        for (uint32_t it = 0; it < a.iters; ++it) {
+            for (uint32_t col = 0; col < a.ncolors; ++col) {
+                const uint32_t off = a.color_ranges[2 * col], cnt = a.color_ranges[2 * col + 1];
+                if (live) for (uint32_t k = sl; k < cnt; k += G) solve_constraint(a, s, off + k);
+                __syncthreads();
+            }
+        }
+        // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
+        for (uint32_t it = 0; it < a.iters; ++it) {
+            for (uint32_t lv = 1; lv <= max_lev; ++lv) {
+                if (live && lv <= my_lev) {
+                    const uint32_t beg = lv == 1 ? 0u : s.loff[lv - 1];
+                    const uint32_t end = s.loff[lv];
+                    for (uint32_t q = beg + sl; q < end; q += G) solve_contact(a, s, &s.con[s.perm[s.order[q]]]);
+                }
+                __syncthreads();
+            }
+        }
+        // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
+        if (live) {
+            const float inv_dt = 1.0f / a.dt;
+            for (uint32_t b = sl; b < B; b += G) {
+                if (a.invmi[b].x < 1e-8f) continue;
+                s.vel[b] = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
+                q4 dq = qmul(toq(s.quat[b]), qconj(toq(s.pquat[b])));
+                if (dq.w < 0) dq = qneg(dq);
+                s.angvel[b] = tof4(scale(sscale(2.0f, xyz(dq)), inv_dt), 0.0f);
+            }
+        }
+        __syncthreads();
+        // ---- K: update_joint_states (:1550-1638) ------------------------------------
+        if (live) {
+            for (uint32_t j = sl; j < a.J; j += G) {
+                const JointRec& jr = a.joints[j];
+                const uint32_t type = (uint32_t)jr.params[0];
+                const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
+                float jp = 0.0f, jv = 0.0f;
+                const q4 q_a = toq(s.quat[ja]), q_b = toq(s.quat[jb]);
+                if (type == JOINT_REVOLUTE) {
+                    const f3 axis_local = mk3(jr.axis[0], jr.axis[1], jr.axis[2]);
+                    const f3 aw = qrot(axis_local, q_a);
+                    const q4 q_rel = qmul(qconj(q_a), q_b);
+                    jp = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
+                    jv = dot(sub(xyz(s.angvel[jb]), xyz(s.angvel[ja])), aw);
+                } else if (type == JOINT_PRISMATIC) {
+                    const f3 aw = qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), q_a);
+                    const f3 r_a = qrot(mk3(jr.anchor_parent[0], jr.anchor_parent[1], jr.anchor_parent[2]), q_a);
+                    const f3 r_b = qrot(mk3(jr.anchor_child[0], jr.anchor_child[1], jr.anchor_child[2]), q_b);
+                    jp = dot(sub(add(xyz(s.pos[jb]), r_b), add(xyz(s.pos[ja]), r_a)), aw);
+                    const f3 vpa = add(xyz(s.vel[ja]), cross(xyz(s.angvel[ja]), r_a));
+                    const f3 vpb = add(xyz(s.vel[jb]), cross(xyz(s.angvel[jb]), r_b));
+                    jv = dot(sub(vpb, vpa), aw);
+                }
+                s.jp[j] = jp;
+                s.jv[j] = jv;
+            }
+        }
+        __syncthreads();
+        // ---- L: read_sensors (:1799-1893); cache_contacts is the next snapshot --------
+        if (stepped && step + 1 == a.substeps) {
+            float* obs = a.obs + (size_t)env * a.obsp;
+            for (uint32_t k = sl; k < a.S; k += G) {
+                const SensorRec& sr = a.sensors[k];
+                const uint32_t obj = sr.type_object[1];
+                float* o = obs + (uint32_t)sr.params[3];
+                switch (sr.type_object[0]) {
+                    case S_JOINT_POS: o[0] = s.jp[obj]; break;
+                    case S_JOINT_VEL: o[0] = s.jv[obj]; break;
+                    case S_ACCELEROMETER: {
+                        f3 lg = qrot(mk3(a.gx, a.gy, a.gz), qconj(toq(s.quat[obj])));
+                        o[0] = lg.x; o[1] = lg.y; o[2] = lg.z;
+                        break;
+                    }
+                    case S_GYRO: case S_FRAMEANGVEL: { float4 w = s.angvel[obj]; o[0] = w.x; o[1] = w.y; o[2] = w.z; break; }
+                    case S_FRAMEPOS: { float4 p = s.pos[obj]; o[0] = p.x; o[1] = p.y; o[2] = p.z; break; }
+                    case S_FRAMEQUAT: { float4 q = s.quat[obj]; o[0] = q.x; o[1] = q.y; o[2] = q.z; o[3] = q.w; break; }
+                    case S_FRAMELINVEL: { float4 v = s.vel[obj]; o[0] = v.x; o[1] = v.y; o[2] = v.z; break; }
+                    default: break;
+                }
+            }
+        }
+        pcount = count;
+        __syncthreads();
+    }
+
+    // ---- Write back (LDS -> HBM) ------------------------------------------------------
+    if (!live) return;
+    const uint32_t n_out = count < M ? count : M;
+    if (stepped) {
+        const size_t eb = (size_t)env * B;
+        for (uint32_t b = sl; b < B; b += G) {
+            a.pos[eb + b] = s.pos[b];
+            a.quat[eb + b] = s.quat[b];
+            const float4 v = s.vel[b], v0 = s.vb[b];
+            a.vel[eb + b] = v;
+            a.angvel[eb + b] = s.angvel[b];
+            a.acc[eb + b] = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+        }
+        for (uint32_t j = sl; j < a.J; j += G) {
+            const size_t o = (size_t)env * Jp + j;
+            a.jtrq[o] = s.jt[j];
+            a.jpos[o] = s.jp[j];
+            a.jvel[o] = s.jv[j];
+        }
+        ContactRec* gc = a.contacts + (size_t)env * M;
+        for (uint32_t k = sl; k < n_out; k += G) {
+            const float4* src = (const float4*)&s.con[s.perm[k]];
+            float4* d = (float4*)&gc[k];
+            d[0] = src[0]; d[1] = src[1]; d[2] = src[2]; d[3] = src[3];
+        }
+        if (sl == 0) a.counts[env] = count;
+    } else {
+        // Not advanced: keep visible state, record the advanced contact list as the
+        // previous-contact snapshot (world.zig:880-928 restores everything else).
+        ContactRec* pc = a.prev_out + (size_t)env * M;
+        for (uint32_t k = sl; k < n_out; k += G) {
+            const float4* src = (const float4*)&s.con[s.perm[k]];
+            float4* d = (float4*)&pc[k];
+            d[0] = src[0]; d[1] = src[1]; d[2] = src[2]; d[3] = src[3];
+        }
+    }
+    for (uint32_t i = sl; i < N; i += G) a.lam[(size_t)env * N + i] = s.lam[i];
+    if (sl == 0) {
+        a.pcounts[env] = count;
+        if (a.prev_detached_out) a.prev_detached_out[env] = stepped ? 0 : 1;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
+    if (a.E == 0) return hipSuccess;
+    const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
+    const size_t shmem = (size_t)a.lds.bytes * (size_t)envs_per_wave;
+    switch (envs_per_wave) {
+        case 1: hipLaunchKernelGGL(step_kernel<1>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 2: hipLaunchKernelGGL(step_kernel<2>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 4: hipLaunchKernelGGL(step_kernel<4>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 8: hipLaunchKernelGGL(step_kernel<8>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace za

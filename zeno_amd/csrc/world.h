@@ -1,0 +1,103 @@
+// World: one batched simulation on one GPU (the MI355X counterpart of src/world/world.zig).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/zeno.h"
+#include "model.h"
+#include "step.h"
+
+namespace za {
+
+// Host mirror ids (one pinned buffer each, refreshed lazily after device work).
+enum MirrorId {
+    MIR_POS, MIR_QUAT, MIR_VEL, MIR_ANGVEL, MIR_ACC, MIR_JPOS, MIR_JVEL, MIR_JTRQ, MIR_OBS,
+    MIR_CON, MIR_COUNT, MIR_COUNT_ALL
+};
+
+struct World {
+    Model model;
+    uint32_t E = 0, B = 0, J = 0, Jp = 1, A = 0, Ap = 1, obsp = 1, N = 0, M = 0;
+    uint32_t iters = 4, cfg_substeps = 1, adaptive_substeps = 1;
+    uint64_t seed = 42;
+    bool profiling = false;
+    float timestep = 0.002f;  // WorldConfig.timestep (full step)
+    float dt = 0.002f;        // SimParams.dt of the last step
+    float gravity[3] = {0, 0, -9.81f};
+    int device = 0;
+    int epw = 1;
+    EnvLds lds{};
+    hipStream_t stream = nullptr;
+    size_t device_bytes = 0;
+
+    // Model on device.
+    float4 *d_invmi = nullptr, *d_com = nullptr;
+    uint32_t* d_kin = nullptr;
+    JointRec* d_joints = nullptr;
+    GeomRec* d_geoms = nullptr;
+    ActuatorRec* d_acts = nullptr;
+    SensorRec* d_sensors = nullptr;
+    ConstraintRec* d_tmpl = nullptr;
+    uint32_t *d_ranges = nullptr, *d_pairs = nullptr;
+    float4 *d_init_pos = nullptr, *d_init_quat = nullptr, *d_init_vel = nullptr, *d_init_angvel = nullptr;
+
+    // State on device (reference layouts).
+    float4 *d_pos = nullptr, *d_quat = nullptr, *d_vel = nullptr, *d_angvel = nullptr, *d_acc = nullptr;
+    float *d_jpos = nullptr, *d_jvel = nullptr, *d_jtrq = nullptr, *d_obs = nullptr, *d_lam = nullptr;
+    float* d_actions = nullptr;
+    ContactRec* d_con = nullptr;
+    uint32_t *d_counts = nullptr, *d_pcounts = nullptr;
+    // step_subset support, allocated on first use.
+    ContactRec* d_prev_con = nullptr;
+    uint8_t* d_prev_detached = nullptr;
+    uint8_t* d_mask = nullptr;
+    float4* d_stage = nullptr;  // [E*B] staging for masked state writes
+
+    // Host mirrors.
+    void* h_mirror[MIR_COUNT_ALL] = {};
+    size_t mirror_bytes[MIR_COUNT_ALL] = {};
+    bool dirty[MIR_COUNT_ALL] = {};
+    float* h_rewards = nullptr;
+    uint8_t* h_dones = nullptr;
+
+    // Pinned action staging ring.
+    static constexpr int kStage = 3;
+    float* h_act[kStage] = {};
+    hipEvent_t act_evt[kStage] = {};
+    bool act_evt_used[kStage] = {};
+    int act_slot = 0;
+    uint8_t* h_mask_stage = nullptr;
+
+    // Profiling and kernel timing.
+    hipEvent_t prof_start = nullptr, prof_stop = nullptr;
+    bool prof_pending = false;
+    ZenoProfilingData prof{};
+    bool timing = false;
+    std::vector<hipEvent_t> t_events;  // pairs
+    size_t t_used = 0;                 // events used (2 per launch)
+
+    ~World();
+    static World* create(const Scene& scene, const ZenoConfig& cfg, std::string& err);
+
+    hipError_t step(const float* actions, uint32_t substeps, bool actions_on_device);
+    hipError_t step_subset(const float* actions, const uint8_t* mask, uint32_t substeps);
+    hipError_t reset(const uint8_t* mask);
+    hipError_t reset_to_state(const float* pos, const float* quat, const float* vel, const float* angvel,
+                              const uint8_t* mask);
+    hipError_t set_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask);
+    void* mirror(MirrorId id);
+    hipError_t sync();
+    hipError_t get_profiling(ZenoProfilingData* out);
+    hipError_t kernel_timing(double* ms, uint64_t* launches);
+    uint64_t state_bytes() const;
+
+   private:
+    hipError_t launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask);
+    hipError_t upload_mask(const uint8_t* mask, uint8_t** d_out);
+    hipError_t ensure_subset_buffers();
+    void mark_all_dirty();
+};
+
+}  // namespace za

@@ -1,0 +1,472 @@
+// World lifecycle, stepping and state access on one GPU.
+//
+// Mirrors World in src/world/world.zig: init (:215-691), step (:694-792), stepSubset
+// (:833-929), reset (:1296-1314), setters (:1413-1478), and the reset_to_state path of
+// src/main.zig:290-385. State stays in HBM; host pointers handed to callers are pinned
+// mirrors refreshed on demand.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "world.h"
+
+#define ZA_TRY(x)                                   \
+    do {                                            \
+        hipError_t _e = (x);                        \
+        if (_e != hipSuccess) return _e;            \
+    } while (0)
+
+namespace za {
+namespace {
+
+// reset (world.zig:1296-1310 with state.zig:390-411): restore the captured initial body
+// state and zero joint positions / velocities of the selected envs.
+__global__ void reset_envs_kernel(uint32_t E, uint32_t B, uint32_t J, uint32_t Jp, const uint8_t* mask,
+                                  const float4* ipos, const float4* iquat, const float4* ivel, const float4* iang,
+                                  float4* pos, float4* quat, float4* vel, float4* ang, float* jpos, float* jvel) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t per = B + J;
+    if (i >= E * per) return;
+    const uint32_t e = i / per, k = i % per;
+    if (mask && !mask[e]) return;
+    if (k < B) {
+        const size_t o = (size_t)e * B + k;
+        pos[o] = ipos[k];
+        quat[o] = iquat[k];
+        vel[o] = ivel[k];
+        ang[o] = iang[k];
+    } else {
+        const size_t o = (size_t)e * Jp + (k - B);
+        jpos[o] = 0.0f;
+        jvel[o] = 0.0f;
+    }
+}
+
+// Copies src into dst for the envs selected by mask (all envs when mask is null).
+__global__ void masked_copy_kernel(uint32_t E, uint32_t B, const uint8_t* mask, const float4* src, float4* dst) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= E * B) return;
+    if (mask && !mask[i / B]) return;
+    dst[i] = src[i];
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t n, uint32_t v) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void fill_u8_kernel(uint8_t* p, uint32_t n, uint8_t v) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+inline uint32_t blocks_for(uint64_t n, uint32_t t) { return (uint32_t)((n + t - 1) / t); }
+
+template <typename T>
+hipError_t dalloc(World* w, T** p, size_t count) {
+    size_t bytes = std::max<size_t>(count, 1) * sizeof(T);
+    hipError_t e = hipMalloc((void**)p, bytes);
+    if (e == hipSuccess) w->device_bytes += bytes;
+    return e;
+}
+
+template <typename T>
+hipError_t upload(World* w, T** p, const T* src, size_t count) {
+    ZA_TRY(dalloc(w, p, count));
+    if (count) ZA_TRY(hipMemcpy(*p, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return hipSuccess;
+}
+
+hipError_t fill_u32(hipStream_t s, uint32_t* p, uint32_t n, uint32_t v) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+World::~World() {
+    if (stream) hipStreamSynchronize(stream);
+    void* dev[] = {d_invmi, d_com, d_kin, d_joints, d_geoms, d_acts, d_sensors, d_tmpl, d_ranges, d_pairs,
+                   d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
+                   d_jpos, d_jvel, d_jtrq, d_obs, d_lam, d_actions, d_con, d_counts, d_pcounts, d_prev_con,
+                   d_prev_detached, d_mask, d_stage};
+    for (void* p : dev) if (p) hipFree(p);
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) if (h_mirror[i]) hipHostFree(h_mirror[i]);
+    for (int i = 0; i < kStage; ++i) {
+        if (h_act[i]) hipHostFree(h_act[i]);
+        if (act_evt[i]) hipEventDestroy(act_evt[i]);
+    }
+    if (h_mask_stage) hipHostFree(h_mask_stage);
+    std::free(h_rewards);
+    std::free(h_dones);
+    if (prof_start) hipEventDestroy(prof_start);
+    if (prof_stop) hipEventDestroy(prof_stop);
+    for (hipEvent_t ev : t_events) hipEventDestroy(ev);
+    if (stream) hipStreamDestroy(stream);
+}
+
+World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err) {
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+        err = "no HIP device available";
+        return nullptr;
+    }
+    World* w = new World();
+    auto fail = [&](const char* what, hipError_t e) -> World* {
+        err = std::string(what) + ": " + hipGetErrorString(e);
+        delete w;
+        return nullptr;
+    };
+    build_model(scene, w->model);
+    const Model& m = w->model;
+    w->E = cfg.num_envs;
+    w->B = m.num_bodies;
+    w->J = m.num_joints;
+    w->Jp = std::max<uint32_t>(m.num_joints, 1);
+    w->A = m.num_actuators;
+    w->Ap = std::max<uint32_t>(m.num_actuators, 1);
+    w->obsp = std::max<uint32_t>(m.obs_dim, 1);
+    w->N = m.num_constraints;
+    w->M = cfg.max_contacts_per_env;
+    w->iters = cfg.contact_iterations;
+    w->cfg_substeps = cfg.substeps;
+    w->adaptive_substeps = cfg.substeps;
+    w->seed = cfg.seed;
+    w->profiling = cfg.enable_profiling;
+    // main.zig:153: 0 (or negative) selects the MJCF timestep.
+    w->timestep = cfg.timestep > 0 ? cfg.timestep : m.physics.timestep;
+    w->dt = w->timestep / (float)std::max<uint32_t>(cfg.substeps, 1);
+    std::memcpy(w->gravity, m.physics.gravity, sizeof w->gravity);
+    if (w->E == 0) { err = "num_envs must be > 0"; delete w; return nullptr; }
+    if (w->B > 65535 || w->M > 65535 || m.num_geoms > 65535) { err = "scene too large"; delete w; return nullptr; }
+
+    hipError_t e = hipGetDevice(&w->device);
+    if (e != hipSuccess) return fail("hipGetDevice", e);
+
+    // Launch shape: the largest environments-per-wave that keeps at least ~one wave per
+    // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS.
+    const EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1));
+    w->lds = L;
+    int epw = 1;
+    for (int cand : {8, 4, 2}) {
+        if (w->M > max_contacts_for(cand)) continue;
+        if ((size_t)L.bytes * cand > 64 * 1024) continue;
+        if ((w->E + cand - 1) / cand < 1024) continue;
+        epw = cand;
+        break;
+    }
+    if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) {
+        int v = std::atoi(env);
+        if (v == 1 || v == 2 || v == 4 || v == 8) epw = v;
+    }
+    if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
+    if ((size_t)L.bytes * epw > 64 * 1024) {
+        err = "per-environment working set exceeds the LDS budget";
+        delete w;
+        return nullptr;
+    }
+    w->epw = epw;
+
+    if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
+
+    // Model.
+    std::vector<float4> invmi(w->B), com(w->B), ip(w->B), iq(w->B), iv(w->B), ia(w->B);
+    std::vector<uint32_t> kin(w->B);
+    for (uint32_t b = 0; b < w->B; ++b) {
+        invmi[b] = make_float4(m.inv_mass_inertia[4 * b], m.inv_mass_inertia[4 * b + 1], m.inv_mass_inertia[4 * b + 2], m.inv_mass_inertia[4 * b + 3]);
+        com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
+        kin[b] = (uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u;
+        ip[b] = make_float4(m.init_pos[4 * b], m.init_pos[4 * b + 1], m.init_pos[4 * b + 2], m.init_pos[4 * b + 3]);
+        iq[b] = make_float4(m.init_quat[4 * b], m.init_quat[4 * b + 1], m.init_quat[4 * b + 2], m.init_quat[4 * b + 3]);
+        iv[b] = make_float4(m.init_vel[4 * b], m.init_vel[4 * b + 1], m.init_vel[4 * b + 2], m.init_vel[4 * b + 3]);
+        ia[b] = make_float4(m.init_angvel[4 * b], m.init_angvel[4 * b + 1], m.init_angvel[4 * b + 2], m.init_angvel[4 * b + 3]);
+    }
+    if ((e = upload(w, &w->d_invmi, invmi.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_com, com.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_kin, kin.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_init_pos, ip.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_init_quat, iq.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_init_vel, iv.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_init_angvel, ia.data(), w->B)) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_joints, m.joints.data(), m.joints.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_geoms, m.geoms.data(), m.geoms.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_acts, m.actuators.data(), m.actuators.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_sensors, m.sensors.data(), m.sensors.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_tmpl, m.templates.data(), m.templates.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_ranges, m.color_ranges.data(), m.color_ranges.size())) != hipSuccess) return fail("upload", e);
+    if ((e = upload(w, &w->d_pairs, m.pairs.data(), m.pairs.size())) != hipSuccess) return fail("upload", e);
+
+    // State (state.zig:56-117 sizes; zero-filled like fresh Metal buffers).
+    const size_t EB = (size_t)w->E * w->B;
+    float4** f4s[] = {&w->d_pos, &w->d_quat, &w->d_vel, &w->d_angvel, &w->d_acc};
+    for (float4** p : f4s) if ((e = dalloc(w, p, EB)) != hipSuccess) return fail("hipMalloc", e);
+    float** fjs[] = {&w->d_jpos, &w->d_jvel, &w->d_jtrq};
+    for (float** p : fjs) if ((e = dalloc(w, p, (size_t)w->E * w->Jp)) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_obs, (size_t)w->E * w->obsp)) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_lam, (size_t)w->E * std::max<uint32_t>(w->N, 1))) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_actions, (size_t)w->E * w->Ap)) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_con, (size_t)w->E * std::max<uint32_t>(w->M, 1))) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_counts, w->E)) != hipSuccess) return fail("hipMalloc", e);
+    if ((e = dalloc(w, &w->d_pcounts, w->E)) != hipSuccess) return fail("hipMalloc", e);
+    struct Z { void* p; size_t n; } zeros[] = {
+        {w->d_pos, EB * 16}, {w->d_quat, EB * 16}, {w->d_vel, EB * 16}, {w->d_angvel, EB * 16}, {w->d_acc, EB * 16},
+        {w->d_jpos, (size_t)w->E * w->Jp * 4}, {w->d_jvel, (size_t)w->E * w->Jp * 4}, {w->d_jtrq, (size_t)w->E * w->Jp * 4},
+        {w->d_obs, (size_t)w->E * w->obsp * 4}, {w->d_lam, (size_t)w->E * std::max<uint32_t>(w->N, 1) * 4},
+        {w->d_actions, (size_t)w->E * w->Ap * 4}, {w->d_con, (size_t)w->E * std::max<uint32_t>(w->M, 1) * 64},
+        {w->d_counts, (size_t)w->E * 4}, {w->d_pcounts, (size_t)w->E * 4}};
+    for (const Z& z : zeros) if ((e = hipMemsetAsync(z.p, 0, z.n, w->stream)) != hipSuccess) return fail("hipMemset", e);
+    // initializeState (world.zig:663-691): every env starts from the scene pose.
+    hipLaunchKernelGGL(reset_envs_kernel, dim3(blocks_for((uint64_t)w->E * (w->B + w->J), 256)), dim3(256), 0, w->stream,
+                       w->E, w->B, w->J, w->Jp, (const uint8_t*)nullptr, w->d_init_pos, w->d_init_quat, w->d_init_vel,
+                       w->d_init_angvel, w->d_pos, w->d_quat, w->d_vel, w->d_angvel, w->d_jpos, w->d_jvel);
+    if ((e = hipGetLastError()) != hipSuccess) return fail("init kernel", e);
+
+    // Host mirrors.
+    const size_t mb[MIR_COUNT_ALL] = {EB * 16, EB * 16, EB * 16, EB * 16, EB * 16,
+                                      (size_t)w->E * w->Jp * 4, (size_t)w->E * w->Jp * 4, (size_t)w->E * w->Jp * 4,
+                                      (size_t)w->E * w->obsp * 4, (size_t)w->E * std::max<uint32_t>(w->M, 1) * 64,
+                                      (size_t)w->E * 4};
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) {
+        w->mirror_bytes[i] = mb[i];
+        if ((e = hipHostMalloc(&w->h_mirror[i], mb[i], hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
+        w->dirty[i] = true;
+    }
+    w->h_rewards = (float*)std::calloc(w->E, sizeof(float));
+    w->h_dones = (uint8_t*)std::calloc(w->E, 1);
+    for (int i = 0; i < kStage; ++i) {
+        if ((e = hipHostMalloc((void**)&w->h_act[i], (size_t)w->E * w->Ap * 4, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
+        if ((e = hipEventCreateWithFlags(&w->act_evt[i], hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
+    }
+    if ((e = hipHostMalloc((void**)&w->h_mask_stage, w->E, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
+    if ((e = hipStreamSynchronize(w->stream)) != hipSuccess) return fail("init", e);
+    return w;
+}
+
+void World::mark_all_dirty() {
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) dirty[i] = true;
+}
+
+hipError_t World::sync() { return hipStreamSynchronize(stream); }
+
+uint64_t World::state_bytes() const { return device_bytes; }
+
+hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask) {
+    StepArgs a{};
+    a.E = E; a.B = B; a.J = J; a.Jp = Jp; a.A = A; a.S = model.num_sensors; a.obsp = obsp; a.N = N;
+    a.ncolors = model.num_colors; a.M = M; a.P = model.num_pairs;
+    a.iters = iters; a.substeps = substeps;
+    a.dt = dt;
+    a.inv_step = timestep > 0 ? 1.0f / timestep : 0.0f;
+    a.gx = gravity[0]; a.gy = gravity[1]; a.gz = gravity[2];
+    a.restitution = model.physics.restitution;
+    a.baumgarte = model.physics.baumgarte;
+    a.slop = model.physics.slop;
+    a.invmi = d_invmi; a.com = d_com; a.kinematic = d_kin; a.joints = d_joints; a.geoms = d_geoms;
+    a.acts = d_acts; a.sensors = d_sensors; a.tmpl = d_tmpl; a.color_ranges = d_ranges; a.pairs = d_pairs;
+    a.pos = d_pos; a.quat = d_quat; a.vel = d_vel; a.angvel = d_angvel; a.acc = d_acc;
+    a.jpos = d_jpos; a.jvel = d_jvel; a.jtrq = d_jtrq; a.obs = d_obs; a.lam = d_lam; a.actions = d_act;
+    a.contacts = d_con; a.counts = d_counts; a.pcounts = d_pcounts;
+    a.prev_detached = d_prev_detached;
+    a.prev_contacts = d_prev_con;
+    a.step_mask = d_step_mask;
+    a.prev_out = d_prev_con;
+    a.prev_detached_out = d_prev_detached;
+    a.lds = lds;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (timing) {
+        while (t_events.size() < t_used + 2) {
+            hipEvent_t ev;
+            ZA_TRY(hipEventCreate(&ev));
+            t_events.push_back(ev);
+        }
+        t0 = t_events[t_used];
+        t1 = t_events[t_used + 1];
+        t_used += 2;
+        ZA_TRY(hipEventRecord(t0, stream));
+    }
+    if (profiling) {
+        if (!prof_start) { ZA_TRY(hipEventCreate(&prof_start)); ZA_TRY(hipEventCreate(&prof_stop)); }
+        ZA_TRY(hipEventRecord(prof_start, stream));
+    }
+    ZA_TRY(launch_step(a, epw, stream));
+    if (profiling) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
+    if (timing) ZA_TRY(hipEventRecord(t1, stream));
+    mark_all_dirty();
+    return hipSuccess;
+}
+
+// World.step, world.zig:694-746: substeps 0 selects the configured count; dt = timestep /
+// substeps; accelerations come from the velocity change over the whole call.
+hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_device) {
+    ZA_TRY(hipSetDevice(device));
+    const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
+    dt = timestep / (float)std::max<uint32_t>(actual, 1);
+    const float* d_act = d_actions;
+    if (actions_on_device) {
+        d_act = actions;
+    } else if (A > 0) {
+        const int slot = act_slot;
+        act_slot = (act_slot + 1) % kStage;
+        if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
+        std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
+        ZA_TRY(hipMemcpyAsync(d_actions, h_act[slot], (size_t)E * A * sizeof(float), hipMemcpyHostToDevice, stream));
+        ZA_TRY(hipEventRecord(act_evt[slot], stream));
+        act_evt_used[slot] = true;
+    }
+    return launch(d_act, actual, nullptr);
+}
+
+hipError_t World::ensure_subset_buffers() {
+    if (!d_prev_con) {
+        ZA_TRY(dalloc(this, &d_prev_con, (size_t)E * std::max<uint32_t>(M, 1)));
+        ZA_TRY(dalloc(this, &d_prev_detached, E));
+        hipLaunchKernelGGL(fill_u8_kernel, dim3(blocks_for(E, 256)), dim3(256), 0, stream, d_prev_detached, E, (uint8_t)0);
+        ZA_TRY(hipGetLastError());
+    }
+    return hipSuccess;
+}
+
+hipError_t World::upload_mask(const uint8_t* mask, uint8_t** d_out) {
+    if (!mask) { *d_out = nullptr; return hipSuccess; }
+    if (!d_mask) ZA_TRY(dalloc(this, &d_mask, E));
+    ZA_TRY(hipStreamSynchronize(stream));  // h_mask_stage may still feed an earlier copy
+    std::memcpy(h_mask_stage, mask, E);
+    ZA_TRY(hipMemcpyAsync(d_mask, h_mask_stage, E, hipMemcpyHostToDevice, stream));
+    *d_out = d_mask;
+    return hipSuccess;
+}
+
+// World.stepSubset, world.zig:833-929: the selected envs advance; the others keep every
+// visible buffer while their solver history (lambda, previous contacts) advances.
+hipError_t World::step_subset(const float* actions, const uint8_t* mask, uint32_t substeps) {
+    ZA_TRY(hipSetDevice(device));
+    uint32_t active = 0;
+    for (uint32_t e = 0; e < E; ++e) active += mask[e] ? 1u : 0u;
+    if (active == 0) return hipSuccess;
+    if (active == E) return step(actions, substeps, false);
+    ZA_TRY(ensure_subset_buffers());
+    const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
+    dt = timestep / (float)std::max<uint32_t>(actual, 1);
+    if (A > 0) {
+        const int slot = act_slot;
+        act_slot = (act_slot + 1) % kStage;
+        if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
+        std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
+        ZA_TRY(hipMemcpyAsync(d_actions, h_act[slot], (size_t)E * A * sizeof(float), hipMemcpyHostToDevice, stream));
+        ZA_TRY(hipEventRecord(act_evt[slot], stream));
+        act_evt_used[slot] = true;
+    }
+    uint8_t* dm = nullptr;
+    ZA_TRY(upload_mask(mask, &dm));
+    return launch(d_actions, actual, dm);
+}
+
+// World.reset, world.zig:1296-1314: restore the selected envs, then zero every env's
+// contact count (the reference clears all counts whatever the mask).
+hipError_t World::reset(const uint8_t* mask) {
+    ZA_TRY(hipSetDevice(device));
+    uint8_t* dm = nullptr;
+    ZA_TRY(upload_mask(mask, &dm));
+    hipLaunchKernelGGL(reset_envs_kernel, dim3(blocks_for((uint64_t)E * (B + J), 256)), dim3(256), 0, stream,
+                       E, B, J, Jp, (const uint8_t*)dm, d_init_pos, d_init_quat, d_init_vel, d_init_angvel,
+                       d_pos, d_quat, d_vel, d_angvel, d_jpos, d_jvel);
+    ZA_TRY(hipGetLastError());
+    ZA_TRY(fill_u32(stream, d_counts, E, 0));
+    mark_all_dirty();
+    return hipSuccess;
+}
+
+hipError_t World::set_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask) {
+    const size_t bytes = (size_t)E * B * 16;
+    if (!mask) {
+        ZA_TRY(hipStreamSynchronize(stream));
+        ZA_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream));
+    } else {
+        if (!d_stage) ZA_TRY(dalloc(this, &d_stage, (size_t)E * B));
+        uint8_t* dm = nullptr;
+        ZA_TRY(upload_mask(mask, &dm));
+        ZA_TRY(hipMemcpyAsync(d_stage, src, bytes, hipMemcpyHostToDevice, stream));
+        hipLaunchKernelGGL(masked_copy_kernel, dim3(blocks_for((uint64_t)E * B, 256)), dim3(256), 0, stream, E, B,
+                           (const uint8_t*)dm, (const float4*)d_stage, dst);
+        ZA_TRY(hipGetLastError());
+    }
+    // The caller's buffer is only borrowed for this call.
+    ZA_TRY(hipStreamSynchronize(stream));
+    dirty[mid] = true;
+    return hipSuccess;
+}
+
+// main.zig:290-385
+hipError_t World::reset_to_state(const float* pos, const float* quat, const float* vel, const float* angvel,
+                                 const uint8_t* mask) {
+    ZA_TRY(hipSetDevice(device));
+    ZA_TRY(set_state_array(d_pos, MIR_POS, pos, mask));
+    ZA_TRY(set_state_array(d_quat, MIR_QUAT, quat, mask));
+    if (vel) ZA_TRY(set_state_array(d_vel, MIR_VEL, vel, mask));
+    if (angvel) ZA_TRY(set_state_array(d_angvel, MIR_ANGVEL, angvel, mask));
+    ZA_TRY(fill_u32(stream, d_counts, E, 0));
+    dirty[MIR_COUNT] = true;
+    return hipSuccess;
+}
+
+void* World::mirror(MirrorId id) {
+    if (hipSetDevice(device) != hipSuccess) return nullptr;
+    if (dirty[id]) {
+        void* src = nullptr;
+        switch (id) {
+            case MIR_POS: src = d_pos; break;
+            case MIR_QUAT: src = d_quat; break;
+            case MIR_VEL: src = d_vel; break;
+            case MIR_ANGVEL: src = d_angvel; break;
+            case MIR_ACC: src = d_acc; break;
+            case MIR_JPOS: src = d_jpos; break;
+            case MIR_JVEL: src = d_jvel; break;
+            case MIR_JTRQ: src = d_jtrq; break;
+            case MIR_OBS: src = d_obs; break;
+            case MIR_CON: src = d_con; break;
+            case MIR_COUNT: src = d_counts; break;
+            default: return nullptr;
+        }
+        if (hipMemcpyAsync(h_mirror[id], src, mirror_bytes[id], hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+        dirty[id] = false;
+    }
+    return h_mirror[id];
+}
+
+hipError_t World::get_profiling(ZenoProfilingData* out) {
+    if (profiling && prof_pending) {
+        ZA_TRY(hipEventSynchronize(prof_stop));
+        float ms = 0.0f;
+        ZA_TRY(hipEventElapsedTime(&ms, prof_start, prof_stop));
+        prof = ZenoProfilingData{};
+        prof.total_step_ns = ms * 1.0e6f;
+        const uint32_t* counts = (const uint32_t*)mirror(MIR_COUNT);
+        uint64_t total = 0;
+        if (counts) for (uint32_t e = 0; e < E; ++e) total += counts[e];
+        prof.num_contacts = (uint32_t)std::min<uint64_t>(total, 0xFFFFFFFFull);
+        prof.num_active_constraints = N * E;
+        prof_pending = false;
+    }
+    *out = prof;
+    return hipSuccess;
+}
+
+hipError_t World::kernel_timing(double* ms, uint64_t* launches) {
+    ZA_TRY(hipStreamSynchronize(stream));
+    double total = 0.0;
+    for (size_t i = 0; i + 1 < t_used; i += 2) {
+        float x = 0.0f;
+        ZA_TRY(hipEventElapsedTime(&x, t_events[i], t_events[i + 1]));
+        total += x;
+    }
+    *ms = total;
+    *launches = t_used / 2;
+    t_used = 0;
+    return hipSuccess;
+}
+
+}  // namespace za
