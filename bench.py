@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Throughput benchmark of the batched physics step on one MI355X.
+
+Workload: Ant, 4096 envs, MJCF timestep 0.01, substeps 1,
+4 solver iterations, 64 contacts per env; actions i.i.d. U[-1,1] per env and step (seed 0),
+torso height 0.75 + U[-0.1,0.1] and hinge noise U[-0.1,0.1] applied with reset_to_state.
+
+A "step" is one zeno_world_step call on the host actions of that step (the reference's
+method, benchmarks/bench_full_physics.zig:67-83): the per-step host->device action copy is
+inside the timed region. W untimed warm-up steps and a reset precede K timed steps,
+bracketed by a stream synchronisation on both sides.
+
+Printed: one JSON line with value = env-steps/s, a roofline object for the step kernel
+(HIP events on the library's stream over the timed region; algorithmic bytes per env-step
+from the buffer sizes the step must read and write) and a CPU baseline (the scalar C oracle
+on this host's cores over a bounded sample of the same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "env-steps/sec at Ant 4096 envs × 1000 steps; achieved HBM GB/s"
+HBM_PEAK_GBPS = 8000.0
+
+
+def algorithmic_bytes_per_env_step(model: dict, max_contacts: int) -> int:
+    """Minimum HBM bytes one env-step must move in the reference layout: actions (R),
+    body pos/quat/vel/angvel (R+W) + accel (W), joint q/qd/tau (W), lambda (R+W), contact
+    slots (R+W), contact count and previous count, observations (W)."""
+    A, B, J = model["num_actuators"], model["num_bodies"], model["num_joints"]
+    N, obs = model["num_constraints"], model["obs_dim"]
+    return 4 * A + 144 * B + 12 * J + 8 * N + 128 * max_contacts + 8 + 4 * obs
+
+
+def hip_device_buffer(host: np.ndarray):
+    """Copies host into a new device allocation (libamdhip64 via ctypes). Returns (ptr, free)."""
+    hip = C.CDLL("libamdhip64.so")
+    ptr = C.c_void_p()
+    if hip.hipMalloc(C.byref(ptr), C.c_size_t(host.nbytes)) != 0:
+        raise RuntimeError("hipMalloc failed")
+    if hip.hipMemcpy(ptr, C.c_void_p(host.ctypes.data), C.c_size_t(host.nbytes), 1) != 0:
+        raise RuntimeError("hipMemcpy failed")
+    return ptr.value, (lambda: hip.hipFree(ptr))
+
+
+def load_traffic(profile_json: Path):
+    try:
+        d = json.loads(profile_json.read_text())
+        return d.get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
+    from oracle.oracle import OracleWorld
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    o = OracleWorld(model, num_envs)
+    o.reset_to_state(*state)
+    o.step(acts[0], nthreads=threads)  # warm-up
+    steps = 0
+    t0 = time.perf_counter()
+    while steps < acts.shape[0] - 1:
+        o.step(acts[steps + 1], nthreads=threads)
+        steps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": num_envs * steps / dt,
+        "unit": "env-steps/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"scalar C oracle (restatement of the reference MSL step), Ant {num_envs} envs x "
+                  f"{steps} steps of the same seeded inputs, OpenMP over envs, {dt:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="ant", choices=["pendulum", "cartpole", "ant", "humanoid", "pile"])
+    ap.add_argument("--envs", type=int, default=0, help="override the workload's env count")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-device-loop", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the step shards by environment with no cross-GPU "
+              "traffic, and this build targets a single MI355X. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from zeno_amd.scenes import WORKLOADS, workload_inputs
+    from zeno_amd.world import ZenoWorld
+
+    wl = WORKLOADS[args.workload]
+    E = args.envs or wl.num_envs
+    total = args.warmup + args.steps
+    path, xml, model, state, acts = workload_inputs(args.workload, E, total, seed=0)
+    w = ZenoWorld(mjcf_path=path, mjcf_string=xml, num_envs=E)
+    epw, lds = w.launch_config()
+
+    # Warm-up, then reset to the seeded initial state (bench_full_physics.zig:67-72).
+    w.reset_to_state(*state)
+    for k in range(args.warmup):
+        w.step(acts[k])
+    w.reset_to_state(*state)
+    w.synchronize()
+
+    # Timed region: K host-action steps; HIP events around every launch on the world's stream.
+    w.set_kernel_timing(True)
+    w.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        w.step(acts[args.warmup + k])
+    w.synchronize()
+    elapsed = time.perf_counter() - t0
+    kernel_ms, launches = w.get_kernel_timing()
+    w.set_kernel_timing(False)
+    value = E * args.steps / elapsed
+    kernel_avg_s = (kernel_ms / 1e3) / max(launches, 1)
+
+    # Sanity of the run itself.
+    pos = w.get_body_positions(zero_copy=False)
+    finite = bool(np.isfinite(pos).all())
+
+    # Device-resident loop: the same steps with actions already in HBM.
+    device_loop = None
+    if not args.no_device_loop and model["num_actuators"] > 0:
+        flat = np.ascontiguousarray(acts[args.warmup:args.warmup + args.steps]).reshape(-1)
+        dptr, dfree = hip_device_buffer(flat)
+        stride = E * model["num_actuators"] * 4
+        w.reset_to_state(*state)
+        w.synchronize()
+        t1 = time.perf_counter()
+        for k in range(args.steps):
+            rc = w._lib.zeno_amd_world_step_device(w.handle, C.c_void_p(dptr + k * stride), 0)
+            if rc != 0:
+                raise RuntimeError(f"step_device failed: {rc}")
+        w.synchronize()
+        el2 = time.perf_counter() - t1
+        dfree()
+        device_loop = {"value": E * args.steps / el2, "ms_per_step": 1e3 * el2 / args.steps}
+
+    bytes_env_step = algorithmic_bytes_per_env_step(model, w.max_contacts_per_env)
+    bytes_launch = bytes_env_step * E
+    achieved = bytes_launch / kernel_avg_s / 1e9
+    prof = ROOT / "profiles" / f"{args.workload}{E}_hbm_traffic.json"
+    traffic = load_traffic(prof)
+
+    result = {
+        "metric": METRIC if args.workload == "ant" and E == 4096 else f"env-steps/sec at {args.workload} {E} envs",
+        "value": value,
+        "unit": "env-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * elapsed / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded initial-state noise and i.i.d. actions on the reference's MJCF model",
+        "config": {
+            "workload": f"{args.workload} {E} envs x {args.steps} steps (zeno_world_step, host actions)",
+            "model": wl.mjcf, "num_envs": E, "timestep": w.timestep, "substeps": 1,
+            "contact_iterations": 4, "max_contacts_per_env": w.max_contacts_per_env,
+            "envs_per_wave": epw, "lds_bytes_per_workgroup": lds,
+        },
+        "hbm_gbps": bytes_env_step * value / 1e9,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBPS,
+            "traffic": traffic,
+            "kernel": "step_kernel",
+            "kernel_avg_us": kernel_avg_s * 1e6,
+            "algorithmic_bytes_per_env_step": bytes_env_step,
+            "algorithmic_bytes_per_launch": bytes_launch,
+        },
+        "device_resident": device_loop,
+        "finite": finite,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(model, state, acts, E, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

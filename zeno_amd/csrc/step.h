@@ -81,6 +81,9 @@ struct StepArgs {
     EnvLds lds;
 };
 
+// Largest dynamic LDS allocation one workgroup may request on `device`.
+size_t max_lds_per_workgroup(int device);
+
 // Launches ceil(E / envs_per_wave) single-wave workgroups. envs_per_wave in {1,2,4,8}.
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream);
 

@@ -805,12 +805,37 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     }
 }
 
+template <int EPW>
+hipError_t allow_lds(size_t shmem) {
+    // Workgroups above 64 KB of dynamic LDS must opt in per kernel (gfx950 has 160 KB / CU).
+    static size_t granted = 64 * 1024;
+    if (shmem <= granted) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    if (e == hipSuccess) granted = shmem;
+    return e;
+}
+
 }  // namespace
+
+size_t max_lds_per_workgroup(int device) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device) != hipSuccess || v <= 0) return 64 * 1024;
+    return (size_t)v;
+}
 
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
     if (a.E == 0) return hipSuccess;
     const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
     const size_t shmem = (size_t)a.lds.bytes * (size_t)envs_per_wave;
+    hipError_t e = hipSuccess;
+    switch (envs_per_wave) {
+        case 1: e = allow_lds<1>(shmem); break;
+        case 2: e = allow_lds<2>(shmem); break;
+        case 4: e = allow_lds<4>(shmem); break;
+        case 8: e = allow_lds<8>(shmem); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
     switch (envs_per_wave) {
         case 1: hipLaunchKernelGGL(step_kernel<1>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
         case 2: hipLaunchKernelGGL(step_kernel<2>, dim3(blocks), dim3(kWave), shmem, stream, a); break;

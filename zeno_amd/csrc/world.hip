@@ -163,7 +163,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         if (v == 1 || v == 2 || v == 4 || v == 8) epw = v;
     }
     if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
-    if ((size_t)L.bytes * epw > 64 * 1024) {
+    if ((size_t)L.bytes * epw > max_lds_per_workgroup(w->device)) {
         err = "per-environment working set exceeds the LDS budget";
         delete w;
         return nullptr;
