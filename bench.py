@@ -54,6 +54,20 @@ def hip_device_buffer(host: np.ndarray):
     return ptr.value, (lambda: hip.hipFree(ptr))
 
 
+def calibrate_copy(nbytes: int) -> None:
+    hip = C.CDLL("libamdhip64.so")
+    a, b = C.c_void_p(), C.c_void_p()
+    if hip.hipMalloc(C.byref(a), C.c_size_t(nbytes)) or hip.hipMalloc(C.byref(b), C.c_size_t(nbytes)):
+        raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(a, 1, C.c_size_t(nbytes))
+    for _ in range(3):
+        if hip.hipMemcpy(b, a, C.c_size_t(nbytes), 3) != 0:
+            raise RuntimeError("hipMemcpy D2D failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+
+
 def load_traffic(profile_json: Path):
     try:
         d = json.loads(profile_json.read_text())
@@ -97,7 +111,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-device-loop", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run 3 device-to-device copies of this many MiB (a plain copy kernel "
+                         "of known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.calibrate_copy_mib > 0:
+        calibrate_copy(args.calibrate_copy_mib << 20)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the step shards by environment with no cross-GPU "
