@@ -40,7 +40,7 @@ struct Lds {
     uint32_t* skey;
     uint32_t* pkey;
     float4 *ppen, *pimp;
-    uint16_t *order, *loff, *last;
+    uint16_t *order, *last;
     uint32_t* misc;
 };
 
@@ -58,10 +58,39 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.skey = (uint32_t*)(base + L.skey);
     s.pkey = (uint32_t*)(base + L.pkey);
     s.ppen = (float4*)(base + L.ppen); s.pimp = (float4*)(base + L.pimp);
-    s.order = (uint16_t*)(base + L.order); s.loff = (uint16_t*)(base + L.loff);
+    s.order = (uint16_t*)(base + L.order);
     s.last = (uint16_t*)(base + L.last);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
+}
+
+// Model records staged in LDS (see ModelLayout).
+struct Mdl {
+    const float4* invmi;
+    const float4* com;
+    const uint32_t* flags;
+    const JointRec* joints;
+    const GeomRec* geoms;
+    const uint32_t* pairs;
+    const ActuatorRec* acts;
+    const SensorRec* sensors;
+    const ConstraintRec* tmpl;
+    const uint32_t* ranges;
+};
+
+__device__ __forceinline__ Mdl bind_model(const unsigned char* base, const ModelLayout& L) {
+    Mdl m;
+    m.invmi = (const float4*)(base + L.invmi);
+    m.com = (const float4*)(base + L.com);
+    m.flags = (const uint32_t*)(base + L.flags);
+    m.joints = (const JointRec*)(base + L.joints);
+    m.geoms = (const GeomRec*)(base + L.geoms);
+    m.pairs = (const uint32_t*)(base + L.pairs);
+    m.acts = (const ActuatorRec*)(base + L.acts);
+    m.sensors = (const SensorRec*)(base + L.sensors);
+    m.tmpl = (const ConstraintRec*)(base + L.tmpl);
+    m.ranges = (const uint32_t*)(base + L.ranges);
+    return m;
 }
 
 __device__ __forceinline__ void set_xyz(float4* p, f3 v) { p->x = v.x; p->y = v.y; p->z = v.z; }
@@ -69,12 +98,12 @@ __device__ __forceinline__ void set_xyz(float4* p, f3 v) { p->x = v.x; p->y = v.
 // ---------------------------------------------------------------------------------------
 // solve_joints, all_shaders.metal:909-1399, one constraint against LDS body state.
 // ---------------------------------------------------------------------------------------
-__device__ void solve_constraint(const StepArgs& a, const Lds& s, uint32_t ci) {
-    const ConstraintRec& c = a.tmpl[ci];
+__device__ void solve_constraint(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t ci) {
+    const ConstraintRec& c = md.tmpl[ci];
     const uint32_t type = c.indices[3] & 0xFFu;
     if (type > 10) return;
     const uint32_t ia = c.indices[0], ib = c.indices[1];
-    const float4 imi_a = a.invmi[ia], imi_b = a.invmi[ib];
+    const float4 imi_a = md.invmi[ia], imi_b = md.invmi[ib];
     const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
     const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
     if (inv_mass_a + inv_mass_b < 1e-8f) return;
@@ -100,8 +129,8 @@ __device__ void solve_constraint(const StepArgs& a, const Lds& s, uint32_t ci) {
             float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
             s.lam[ci] = lambda_prev + d_lambda;
             f3 impulse = sscale(d_lambda, n);
-            f3 rc_a = sub(r_a, qrot(xyz(a.com[ia]), quat_a));
-            f3 rc_b = sub(r_b, qrot(xyz(a.com[ib]), quat_b));
+            f3 rc_a = sub(r_a, qrot(xyz(md.com[ia]), quat_a));
+            f3 rc_b = sub(r_b, qrot(xyz(md.com[ib]), quat_b));
             if (inv_mass_a > 0) {
                 set_xyz(Pa, add(xyz(*Pa), scale(impulse, inv_mass_a)));
                 *Qa = tof4(qnormalize(qadd(quat_a, qdelta(mul(cross(rc_a, impulse), iI_a), quat_a))));
@@ -249,12 +278,12 @@ __device__ void solve_constraint(const StepArgs& a, const Lds& s, uint32_t ci) {
 // ---------------------------------------------------------------------------------------
 // solve_contacts, all_shaders.metal:1644-1793, one contact record.
 // ---------------------------------------------------------------------------------------
-__device__ void solve_contact(const StepArgs& a, const Lds& s, ContactRec* cr) {
+__device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr) {
     const float4 pp = *(const float4*)cr->position_pen;
     if (pp.w < 0) return;
     const float4 nf = *(const float4*)cr->normal_friction;
     const uint32_t ia = cr->indices[0], ib = cr->indices[1];
-    const float4 imi_a = a.invmi[ia], imi_b = a.invmi[ib];
+    const float4 imi_a = md.invmi[ia], imi_b = md.invmi[ib];
     const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
     const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
     const float inv_mass_sum = inv_mass_a + inv_mass_b;
@@ -321,10 +350,10 @@ __device__ void solve_contact(const StepArgs& a, const Lds& s, ContactRec* cr) {
 // ---------------------------------------------------------------------------------------
 // narrow_phase, all_shaders.metal:751-894, one slot.
 // ---------------------------------------------------------------------------------------
-__device__ void narrow_slot(const StepArgs& a, const Lds& s, ContactRec* c) {
+__device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* c) {
     const uint32_t body_a = c->indices[0], body_b = c->indices[1];
-    const GeomRec& ga = a.geoms[c->indices[2]];
-    const GeomRec& gb = a.geoms[c->indices[3]];
+    const GeomRec& ga = md.geoms[c->indices[2]];
+    const GeomRec& gb = md.geoms[c->indices[3]];
     const f3 pos_a = add(xyz(s.pos[body_a]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
     const f3 pos_b = add(xyz(s.pos[body_b]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
     const uint32_t type_a = ga.type_body[0], type_b = gb.type_body[0];
@@ -393,9 +422,26 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     const int sl = tid % G;
     const uint32_t env = blockIdx.x * EPW + le;
     const bool live = env < a.E;
-    const Lds s = bind_lds(smem + le * a.lds.bytes, a.lds);
+    unsigned char* const env_base = smem + a.ml.bytes;
+    const Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
+    const Mdl md = bind_model(smem, a.ml);
     const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
     const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
+
+    // Phase timer: workgroup 0, lane 0 accumulates wall-clock ticks per phase.
+    const bool timer = a.phase_ticks != nullptr && blockIdx.x == 0 && tid == 0;
+    unsigned long long t_last = timer ? (unsigned long long)wall_clock64() : 0ull;
+    unsigned long long t_acc[kPhaseCount] = {};
+    auto tick = [&](int ph) {
+        if (timer) {
+            unsigned long long t = (unsigned long long)wall_clock64();
+            t_acc[ph] += t - t_last;
+            t_last = t;
+        }
+    };
+
+    // ---- Model records (one blob per scene) -> LDS -------------------------------------
+    for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
 
     // ---- Load the env's working set (HBM -> LDS) --------------------------------------
     uint32_t count = 0, pcount = 0;
@@ -424,6 +470,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
     }
     __syncthreads();
+    tick(PH_LOAD);
 
     for (uint32_t step = 0; step < a.substeps; ++step) {
         // ---- Previous-contact snapshot (cache_contacts of the last substep) -----------
@@ -441,7 +488,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         if (live) {
             for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
             for (uint32_t k = sl; k < a.A; k += G) {
-                const ActuatorRec& act = a.acts[k];
+                const ActuatorRec& act = md.acts[k];
                 float ctrl = clampf(a.actions[(size_t)env * a.A + k], act.params[1], act.params[2]);
                 float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
                 s.jt[(uint32_t)act.params[0]] = torque;
@@ -451,8 +498,8 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- B: compute_forces + update_kinematic (:345-388, :304-339) ----------------
         if (live) {
             for (uint32_t b = sl; b < B; b += G) {
-                const float4 imi = a.invmi[b];
-                if (a.kinematic[b]) {
+                const float4 imi = md.invmi[b];
+                if (md.flags[b] & 1u) {
                     f3 p = add(xyz(s.pos[b]), scale(xyz(s.vel[b]), a.dt));
                     s.pos[b] = tof4(p, 0.0f);
                     q4 q = toq(s.quat[b]);
@@ -466,7 +513,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     float mass = 1.0f / imi.x;
                     f3 force = mk3(a.gx * mass, a.gy * mass, a.gz * mass);
                     s.frc[b] = tof4(force, 0.0f);
-                    f3 cw = qrot(xyz(a.com[b]), toq(s.quat[b]));
+                    f3 cw = qrot(xyz(md.com[b]), toq(s.quat[b]));
                     s.trq[b] = tof4(cross(cw, force), 0.0f);
                 }
             }
@@ -478,7 +525,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 if (b > 0) {
                     float4 f = s.frc[b], t = s.trq[b];
                     for (uint32_t j = 0; j < a.J; ++j) {
-                        const JointRec& jr = a.joints[j];
+                        const JointRec& jr = md.joints[j];
                         const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
                         if (ja != b && jb != b) continue;
                         const float tau = s.jt[j];
@@ -499,7 +546,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- D: integrate (:394-462) -------------------------------------------------
         if (live) {
             for (uint32_t b = sl; b < B; b += G) {
-                const float4 imi = a.invmi[b];
+                const float4 imi = md.invmi[b];
                 if (imi.x < 1e-8f) continue;
                 f3 vel = add(xyz(s.vel[b]), scale(scale(xyz(s.frc[b]), imi.x), a.dt));
                 vel = scale(vel, 0.999f);
@@ -518,6 +565,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
         }
         __syncthreads();
+        tick(PH_FORCES);
         // ---- E: broad_phase (S1), :468-533 -------------------------------------------
         const uint32_t count_before = count;
         {
@@ -528,11 +576,11 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 bool hit = false;
                 uint32_t g = 0, h = 0, ba = 0, bb = 0;
                 if (live && p < a.P) {
-                    const uint32_t pr = a.pairs[p];
+                    const uint32_t pr = md.pairs[p];
                     g = pr & 0xFFFFu;
                     h = pr >> 16;
-                    const GeomRec& ga = a.geoms[g];
-                    const GeomRec& gb = a.geoms[h];
+                    const GeomRec& ga = md.geoms[g];
+                    const GeomRec& gb = md.geoms[h];
                     ba = ga.type_body[1];
                     bb = gb.type_body[1];
                     if (ga.type_body[0] == GEOM_PLANE || gb.type_body[0] == GEOM_PLANE) {
@@ -598,10 +646,11 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
         }
         __syncthreads();
+        tick(PH_BROAD);
         // ---- F: narrow_phase (:751-894) -----------------------------------------------
         const uint32_t n_live = count < M ? count : M;
         if (live) {
-            for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, s, &s.con[s.perm[k]]);
+            for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.perm[k]]);
         }
         __syncthreads();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
@@ -637,69 +686,81 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 }
             }
         }
-        // ---- Contact levels for S4 (one lane per env) --------------------------------
-        if (live && sl == 0) {
-            for (uint32_t b = 0; b < B; ++b) s.last[b] = 0;
-            uint32_t nlev = 0;
-            for (uint32_t k = 0; k < n_live; ++k) {
+        // ---- Contact levels for S4 -----------------------------------------------------
+        // level(slot) = 1 + max level of earlier live slots sharing a body that the solve
+        // writes (inv_m > 1e-8). Running levels in order reproduces the sequential slot
+        // order exactly. The per-slot body pair is packed in parallel; one lane per env then
+        // scans the slots in order.
+        if (live) {
+            for (uint32_t k = sl; k < n_live; k += G) {
                 const ContactRec* c = &s.con[s.perm[k]];
-                uint32_t lv = 0;
+                uint32_t info = 0xFFFFFFFFu;
                 if (!(c->position_pen[3] < 0)) {  // solve_contacts skips only pen < 0 (:1667)
                     const uint32_t ia = c->indices[0], ib = c->indices[1];
-                    const bool da = a.invmi[ia].x > 1e-8f, db = a.invmi[ib].x > 1e-8f;
-                    uint32_t l0 = 0;
-                    if (da) l0 = s.last[ia];
-                    if (db && s.last[ib] > l0) l0 = s.last[ib];
-                    lv = l0 + 1;
-                    if (da) s.last[ia] = (uint16_t)lv;
-                    if (db) s.last[ib] = (uint16_t)lv;
-                    if (lv > nlev) nlev = lv;
+                    info = ((md.flags[ia] & 2u) ? ia : 0xFFFFu) | (((md.flags[ib] & 2u) ? ib : 0xFFFFu) << 16);
                 }
-                s.skey[k] = lv;
+                s.skey[k] = info;
             }
-            // Counting sort of live slots by level: order[loff[L-1] .. loff[L]) = level L.
-            for (uint32_t l = 0; l <= nlev; ++l) s.loff[l] = 0;
-            for (uint32_t k = 0; k < n_live; ++k) if (s.skey[k]) s.loff[s.skey[k]]++;
-            uint32_t run = 0;
-            for (uint32_t l = 0; l <= nlev; ++l) { uint32_t c = s.loff[l]; s.loff[l] = (uint16_t)run; run += c; }
+            for (uint32_t b = sl; b < B; b += G) s.last[b] = 0;
+        }
+        __syncthreads();
+        if (live && sl == 0) {
+            uint32_t nlev = 0;
             for (uint32_t k = 0; k < n_live; ++k) {
-                uint32_t lv = s.skey[k];
-                if (lv) s.order[s.loff[lv]++] = (uint16_t)k;
+                const uint32_t info = s.skey[k];
+                uint32_t lv = 0;
+                if (info != 0xFFFFFFFFu) {
+                    const uint32_t ia = info & 0xFFFFu, ib = info >> 16;
+                    const uint32_t la = ia != 0xFFFFu ? s.last[ia] : 0u;
+                    const uint32_t lb = ib != 0xFFFFu ? s.last[ib] : 0u;
+                    lv = (la > lb ? la : lb) + 1;
+                    if (ia != 0xFFFFu) s.last[ia] = (uint16_t)lv;
+                    if (ib != 0xFFFFu) s.last[ib] = (uint16_t)lv;
+                    nlev = lv > nlev ? lv : nlev;
+                }
+                s.order[k] = (uint16_t)lv;
             }
-            // loff[l] now holds the end of level l; shift so that level L spans [loff[L-1], loff[L]).
             s.misc[2] = nlev;
         }
         __syncthreads();
         uint32_t max_lev = 0;
         for (int e2 = 0; e2 < EPW; ++e2) {
-            const uint32_t* m2 = (const uint32_t*)(smem + e2 * a.lds.bytes + a.lds.misc);
+            const uint32_t* m2 = (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
             if (blockIdx.x * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
         }
-        const uint32_t my_lev = live ? s.misc[2] : 0;
+        // Each lane keeps the level of the slots it owns (sl, sl + G, ...) in registers.
+        uint16_t my_level[kMaxRecsPerLane];
+#pragma unroll
+        for (int r = 0; r < kMaxRecsPerLane; ++r) {
+            const uint32_t k = sl + r * G;
+            my_level[r] = (live && k < n_live) ? s.order[k] : (uint16_t)0;
+        }
+        tick(PH_NARROW);
         // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
         for (uint32_t it = 0; it < a.iters; ++it) {
             for (uint32_t col = 0; col < a.ncolors; ++col) {
-                const uint32_t off = a.color_ranges[2 * col], cnt = a.color_ranges[2 * col + 1];
-                if (live) for (uint32_t k = sl; k < cnt; k += G) solve_constraint(a, s, off + k);
+                const uint32_t off = md.ranges[2 * col], cnt = md.ranges[2 * col + 1];
+                if (live) for (uint32_t k = sl; k < cnt; k += G) solve_constraint(a, md, s, off + k);
                 __syncthreads();
             }
         }
+        tick(PH_JOINTS);
         // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
         for (uint32_t it = 0; it < a.iters; ++it) {
             for (uint32_t lv = 1; lv <= max_lev; ++lv) {
-                if (live && lv <= my_lev) {
-                    const uint32_t beg = lv == 1 ? 0u : s.loff[lv - 1];
-                    const uint32_t end = s.loff[lv];
-                    for (uint32_t q = beg + sl; q < end; q += G) solve_contact(a, s, &s.con[s.perm[s.order[q]]]);
+#pragma unroll
+                for (int r = 0; r < kMaxRecsPerLane; ++r) {
+                    if (my_level[r] == lv) solve_contact(a, md, s, &s.con[s.perm[sl + r * G]]);
                 }
                 __syncthreads();
             }
         }
+        tick(PH_CONTACTS);
         // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
         if (live) {
             const float inv_dt = 1.0f / a.dt;
             for (uint32_t b = sl; b < B; b += G) {
-                if (a.invmi[b].x < 1e-8f) continue;
+                if (md.invmi[b].x < 1e-8f) continue;
                 s.vel[b] = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
                 q4 dq = qmul(toq(s.quat[b]), qconj(toq(s.pquat[b])));
                 if (dq.w < 0) dq = qneg(dq);
@@ -710,7 +771,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- K: update_joint_states (:1550-1638) ------------------------------------
         if (live) {
             for (uint32_t j = sl; j < a.J; j += G) {
-                const JointRec& jr = a.joints[j];
+                const JointRec& jr = md.joints[j];
                 const uint32_t type = (uint32_t)jr.params[0];
                 const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
                 float jp = 0.0f, jv = 0.0f;
@@ -739,7 +800,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         if (stepped && step + 1 == a.substeps) {
             float* obs = a.obs + (size_t)env * a.obsp;
             for (uint32_t k = sl; k < a.S; k += G) {
-                const SensorRec& sr = a.sensors[k];
+                const SensorRec& sr = md.sensors[k];
                 const uint32_t obj = sr.type_object[1];
                 float* o = obs + (uint32_t)sr.params[3];
                 switch (sr.type_object[0]) {
@@ -760,6 +821,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         pcount = count;
         __syncthreads();
+        tick(PH_POST);
     }
 
     // ---- Write back (LDS -> HBM) ------------------------------------------------------
@@ -803,6 +865,10 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         a.pcounts[env] = count;
         if (a.prev_detached_out) a.prev_detached_out[env] = stepped ? 0 : 1;
     }
+    tick(PH_STORE);
+    if (timer) {
+        for (int ph = 0; ph < kPhaseCount; ++ph) a.phase_ticks[ph] = t_acc[ph];
+    }
 }
 
 template <int EPW>
@@ -826,7 +892,7 @@ size_t max_lds_per_workgroup(int device) {
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
     if (a.E == 0) return hipSuccess;
     const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
-    const size_t shmem = (size_t)a.lds.bytes * (size_t)envs_per_wave;
+    const size_t shmem = (size_t)a.ml.bytes + (size_t)a.lds.bytes * (size_t)envs_per_wave;
     hipError_t e = hipSuccess;
     switch (envs_per_wave) {
         case 1: e = allow_lds<1>(shmem); break;

@@ -32,15 +32,9 @@ struct World {
     hipStream_t stream = nullptr;
     size_t device_bytes = 0;
 
-    // Model on device.
-    float4 *d_invmi = nullptr, *d_com = nullptr;
-    uint32_t* d_kin = nullptr;
-    JointRec* d_joints = nullptr;
-    GeomRec* d_geoms = nullptr;
-    ActuatorRec* d_acts = nullptr;
-    SensorRec* d_sensors = nullptr;
-    ConstraintRec* d_tmpl = nullptr;
-    uint32_t *d_ranges = nullptr, *d_pairs = nullptr;
+    // Model on device: one blob laid out by `ml` (copied into LDS by the step kernel).
+    ModelLayout ml{};
+    uint4* d_model = nullptr;
     float4 *d_init_pos = nullptr, *d_init_quat = nullptr, *d_init_vel = nullptr, *d_init_angvel = nullptr;
 
     // State on device (reference layouts).
@@ -73,6 +67,8 @@ struct World {
     // Profiling and kernel timing.
     hipEvent_t prof_start = nullptr, prof_stop = nullptr;
     bool prof_pending = false;
+    unsigned long long* d_phase = nullptr;  // [kPhaseCount] wall-clock ticks of workgroup 0
+    double wall_clock_hz = 100e6;
     ZenoProfilingData prof{};
     bool timing = false;
     std::vector<hipEvent_t> t_events;  // pairs

@@ -89,8 +89,7 @@ hipError_t fill_u32(hipStream_t s, uint32_t* p, uint32_t n, uint32_t v) {
 
 World::~World() {
     if (stream) hipStreamSynchronize(stream);
-    void* dev[] = {d_invmi, d_com, d_kin, d_joints, d_geoms, d_acts, d_sensors, d_tmpl, d_ranges, d_pairs,
-                   d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
+    void* dev[] = {d_model, d_phase, d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
                    d_jpos, d_jvel, d_jtrq, d_obs, d_lam, d_actions, d_con, d_counts, d_pcounts, d_prev_con,
                    d_prev_detached, d_mask, d_stage};
     for (void* p : dev) if (p) hipFree(p);
@@ -150,10 +149,11 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS.
     const EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1));
     w->lds = L;
+    const ModelLayout ML = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->N, m.num_colors);
     int epw = 1;
     for (int cand : {8, 4, 2}) {
         if (w->M > max_contacts_for(cand)) continue;
-        if ((size_t)L.bytes * cand > 64 * 1024) continue;
+        if ((size_t)ML.bytes + (size_t)L.bytes * cand > 64 * 1024) continue;
         if ((w->E + cand - 1) / cand < 1024) continue;
         epw = cand;
         break;
@@ -163,7 +163,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         if (v == 1 || v == 2 || v == 4 || v == 8) epw = v;
     }
     if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
-    if ((size_t)L.bytes * epw > max_lds_per_workgroup(w->device)) {
+    if ((size_t)ML.bytes + (size_t)L.bytes * epw > max_lds_per_workgroup(w->device)) {
         err = "per-environment working set exceeds the LDS budget";
         delete w;
         return nullptr;
@@ -172,32 +172,48 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
 
-    // Model.
-    std::vector<float4> invmi(w->B), com(w->B), ip(w->B), iq(w->B), iv(w->B), ia(w->B);
-    std::vector<uint32_t> kin(w->B);
+    // Model blob: every per-scene record the kernel reads, packed per ModelLayout.
+    w->ml = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->N, m.num_colors);
+    {
+        std::vector<unsigned char> blob(w->ml.bytes, 0);
+        auto put = [&](uint32_t off, const void* src, size_t bytes) { if (bytes) std::memcpy(blob.data() + off, src, bytes); };
+        std::vector<float4> invmi(w->B), com(w->B);
+        std::vector<uint32_t> flags(w->B);
+        for (uint32_t b = 0; b < w->B; ++b) {
+            const float* im = &m.inv_mass_inertia[4 * b];
+            invmi[b] = make_float4(im[0], im[1], im[2], im[3]);
+            com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
+            flags[b] = ((uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u) | (im[0] > 1e-8f ? 2u : 0u);
+        }
+        put(w->ml.invmi, invmi.data(), 16 * w->B);
+        put(w->ml.com, com.data(), 16 * w->B);
+        put(w->ml.flags, flags.data(), 4 * w->B);
+        put(w->ml.joints, m.joints.data(), sizeof(JointRec) * m.joints.size());
+        put(w->ml.geoms, m.geoms.data(), sizeof(GeomRec) * m.geoms.size());
+        put(w->ml.pairs, m.pairs.data(), 4 * m.pairs.size());
+        put(w->ml.acts, m.actuators.data(), sizeof(ActuatorRec) * m.actuators.size());
+        put(w->ml.sensors, m.sensors.data(), sizeof(SensorRec) * m.sensors.size());
+        put(w->ml.tmpl, m.templates.data(), sizeof(ConstraintRec) * m.templates.size());
+        put(w->ml.ranges, m.color_ranges.data(), 4 * m.color_ranges.size());
+        if ((e = upload(w, &w->d_model, (const uint4*)blob.data(), w->ml.bytes / 16)) != hipSuccess) return fail("upload", e);
+    }
+    std::vector<float4> ip(w->B), iq(w->B), iv(w->B), ia(w->B);
     for (uint32_t b = 0; b < w->B; ++b) {
-        invmi[b] = make_float4(m.inv_mass_inertia[4 * b], m.inv_mass_inertia[4 * b + 1], m.inv_mass_inertia[4 * b + 2], m.inv_mass_inertia[4 * b + 3]);
-        com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
-        kin[b] = (uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u;
         ip[b] = make_float4(m.init_pos[4 * b], m.init_pos[4 * b + 1], m.init_pos[4 * b + 2], m.init_pos[4 * b + 3]);
         iq[b] = make_float4(m.init_quat[4 * b], m.init_quat[4 * b + 1], m.init_quat[4 * b + 2], m.init_quat[4 * b + 3]);
         iv[b] = make_float4(m.init_vel[4 * b], m.init_vel[4 * b + 1], m.init_vel[4 * b + 2], m.init_vel[4 * b + 3]);
         ia[b] = make_float4(m.init_angvel[4 * b], m.init_angvel[4 * b + 1], m.init_angvel[4 * b + 2], m.init_angvel[4 * b + 3]);
     }
-    if ((e = upload(w, &w->d_invmi, invmi.data(), w->B)) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_com, com.data(), w->B)) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_kin, kin.data(), w->B)) != hipSuccess) return fail("upload", e);
     if ((e = upload(w, &w->d_init_pos, ip.data(), w->B)) != hipSuccess) return fail("upload", e);
     if ((e = upload(w, &w->d_init_quat, iq.data(), w->B)) != hipSuccess) return fail("upload", e);
     if ((e = upload(w, &w->d_init_vel, iv.data(), w->B)) != hipSuccess) return fail("upload", e);
     if ((e = upload(w, &w->d_init_angvel, ia.data(), w->B)) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_joints, m.joints.data(), m.joints.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_geoms, m.geoms.data(), m.geoms.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_acts, m.actuators.data(), m.actuators.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_sensors, m.sensors.data(), m.sensors.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_tmpl, m.templates.data(), m.templates.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_ranges, m.color_ranges.data(), m.color_ranges.size())) != hipSuccess) return fail("upload", e);
-    if ((e = upload(w, &w->d_pairs, m.pairs.data(), m.pairs.size())) != hipSuccess) return fail("upload", e);
+    if (w->profiling) {
+        if ((e = dalloc(w, &w->d_phase, kPhaseCount)) != hipSuccess) return fail("hipMalloc", e);
+        int khz = 0;
+        if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, w->device) == hipSuccess && khz > 0)
+            w->wall_clock_hz = 1e3 * (double)khz;
+    }
 
     // State (state.zig:56-117 sizes; zero-filled like fresh Metal buffers).
     const size_t EB = (size_t)w->E * w->B;
@@ -264,8 +280,9 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.restitution = model.physics.restitution;
     a.baumgarte = model.physics.baumgarte;
     a.slop = model.physics.slop;
-    a.invmi = d_invmi; a.com = d_com; a.kinematic = d_kin; a.joints = d_joints; a.geoms = d_geoms;
-    a.acts = d_acts; a.sensors = d_sensors; a.tmpl = d_tmpl; a.color_ranges = d_ranges; a.pairs = d_pairs;
+    a.model = d_model;
+    a.ml = ml;
+    a.phase_ticks = profiling ? d_phase : nullptr;
     a.pos = d_pos; a.quat = d_quat; a.vel = d_vel; a.angvel = d_angvel; a.acc = d_acc;
     a.jpos = d_jpos; a.jvel = d_jvel; a.jtrq = d_jtrq; a.obs = d_obs; a.lam = d_lam; a.actions = d_act;
     a.contacts = d_con; a.counts = d_counts; a.pcounts = d_pcounts;
@@ -444,6 +461,14 @@ hipError_t World::get_profiling(ZenoProfilingData* out) {
         ZA_TRY(hipEventElapsedTime(&ms, prof_start, prof_stop));
         prof = ZenoProfilingData{};
         prof.total_step_ns = ms * 1.0e6f;
+        // Per-phase wall-clock time of workgroup 0 (in-kernel s_memrealtime stamps).
+        unsigned long long t[kPhaseCount] = {};
+        ZA_TRY(hipMemcpy(t, d_phase, sizeof t, hipMemcpyDeviceToHost));
+        const double ns = 1e9 / wall_clock_hz;
+        prof.integrate_ns = (float)((double)(t[PH_LOAD] + t[PH_FORCES] + t[PH_POST] + t[PH_STORE]) * ns);
+        prof.collision_broad_ns = (float)((double)t[PH_BROAD] * ns);
+        prof.collision_narrow_ns = (float)((double)t[PH_NARROW] * ns);
+        prof.constraint_solve_ns = (float)((double)(t[PH_JOINTS] + t[PH_CONTACTS]) * ns);
         const uint32_t* counts = (const uint32_t*)mirror(MIR_COUNT);
         uint64_t total = 0;
         if (counts) for (uint32_t e = 0; e < E; ++e) total += counts[e];
