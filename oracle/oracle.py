@@ -61,6 +61,10 @@ def load() -> C.CDLL:
         lib.zo_atan2f.argtypes = [C.c_float, C.c_float]
         lib.zo_asinf.restype = C.c_float
         lib.zo_asinf.argtypes = [C.c_float]
+        lib.zo_match_cached.restype = None
+        lib.zo_match_cached.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]
+        lib.zo_sort_contacts.restype = None
+        lib.zo_sort_contacts.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32]
         lib.zo_collide_env.restype = None
         lib.zo_collide_env.argtypes = [C.POINTER(ZoModel), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         _lib = lib
@@ -187,6 +191,29 @@ class OracleWorld:
 
     def lambdas(self) -> np.ndarray:
         return self.constraints["state"][:, :, 0].copy()
+
+
+def sort_contacts(contacts: np.ndarray, count: int) -> None:
+    """In-place stable insertion sort of one env's contact list (schedule of the reference)."""
+    assert contacts.dtype == CONTACT_DTYPE and contacts.flags["C_CONTIGUOUS"]
+    load().zo_sort_contacts(contacts.shape[0], _p(contacts), count)
+
+
+def match_cached(contacts: np.ndarray, count: int, prev: np.ndarray, prev_count: int) -> None:
+    """In-place warm start of one env's contacts from its previous list."""
+    assert contacts.shape == prev.shape
+    load().zo_match_cached(contacts.shape[0], _p(contacts), count, _p(prev), prev_count)
+
+
+def collide_env(world: "OracleWorld", env: int = 0) -> None:
+    """Broad phase + sort + narrow phase of one env on its current positions."""
+    zm = world._model_struct()
+    cnt = np.array([world.contact_counts[env]], np.uint32)
+    con = np.ascontiguousarray(world.contacts[env])
+    load().zo_collide_env(C.byref(zm), _p(np.ascontiguousarray(world.positions[env])),
+                          _p(np.ascontiguousarray(world.quaternions[env])), _p(con), _p(cnt))
+    world.contacts[env] = con
+    world.contact_counts[env] = cnt[0]
 
 
 def atan2f(y: float, x: float) -> float:

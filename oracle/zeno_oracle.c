@@ -919,6 +919,22 @@ int zo_step(const ZoModel* m, ZoState* s, const float* actions, uint32_t substep
     return 0;
 }
 
+void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,
+                     ZoContact* prev_contacts, uint32_t prev_count) {
+    Env e;
+    memset(&e, 0, sizeof e);
+    e.M = max_contacts;
+    e.con = contacts;
+    e.pcon = prev_contacts;
+    e.count = &count;
+    e.pcount = &prev_count;
+    k_match_cached(&e);
+}
+
+void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count) {
+    k_sort_contacts(max_contacts, contacts, count);
+}
+
 void zo_collide_env(const ZoModel* m, const float* positions, const float* quaternions,
                     ZoContact* contacts, uint32_t* count) {
     (void)quaternions;

@@ -101,6 +101,13 @@ float zo_asinf(float x);
 void zo_collide_env(const ZoModel* m, const float* positions, const float* quaternions,
                     ZoContact* contacts, uint32_t* count);
 
+/* match_cached_contacts (all_shaders.metal:1483-1544) on one env, exposed for unit tests. */
+void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,
+                     ZoContact* prev_contacts, uint32_t prev_count);
+
+/* sort_contacts (all_shaders.metal:711-745) on one env's list, exposed for unit tests. */
+void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count);
+
 #ifdef __cplusplus
 }
 #endif
