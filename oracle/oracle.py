@@ -167,6 +167,36 @@ class OracleWorld:
         end = self.E if env_end is None else env_end
         self.lib.zo_step(C.byref(zm), C.byref(zs), _p(a), substeps, env_begin, end, nthreads)
 
+    _SUBSET_RESTORED = ("positions", "quaternions", "velocities", "accelerations", "angular_velocities",
+                        "joint_positions", "joint_velocities", "joint_torques", "observations",
+                        "contact_counts", "contacts")
+
+    def step_subset(self, actions: Optional[np.ndarray], env_mask, substeps: int = 0) -> None:
+        """World.stepSubset (world.zig:833-929): no active env -> no-op; all active -> step;
+        otherwise back up the per-env outputs, step every env, and restore the unmasked envs'
+        bodies, accelerations, joints, observations, counts and contacts. Constraint lambdas and
+        the prev-contact cache of unmasked envs keep the full step's values."""
+        mask = np.asarray(env_mask).astype(bool)
+        if not mask.any():
+            return
+        if mask.all():
+            self.step(actions, substeps)
+            return
+        backup = {k: getattr(self, k).copy() for k in self._SUBSET_RESTORED}
+        self.step(actions, substeps)
+        keep = ~mask
+        for k, v in backup.items():
+            getattr(self, k)[keep] = v[keep]
+
+    def set_body_positions(self, positions, mask=None) -> None:
+        """World.setBodyPositions: copy the selected envs' positions, nothing else."""
+        sel = np.ones(self.E, bool) if mask is None else np.asarray(mask).astype(bool)
+        self.positions[sel] = np.asarray(positions, np.float32).reshape(self.E, self.B, 4)[sel]
+
+    def set_body_velocities(self, velocities, mask=None) -> None:
+        sel = np.ones(self.E, bool) if mask is None else np.asarray(mask).astype(bool)
+        self.velocities[sel] = np.asarray(velocities, np.float32).reshape(self.E, self.B, 4)[sel]
+
     def reset_to_state(self, positions, quaternions, velocities=None, angular_velocities=None, mask=None):
         """main.zig:290-385: copy the given arrays for the selected envs; zero every count."""
         sel = np.ones(self.E, bool) if mask is None else np.asarray(mask).astype(bool)

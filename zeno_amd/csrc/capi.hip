@@ -207,7 +207,7 @@ int zeno_world_set_gravity(ZenoWorldHandle world, float gx, float gy, float gz) 
 
 int zeno_world_set_timestep(ZenoWorldHandle world, float timestep) {
     if (!world) return ZENO_INVALID_HANDLE;
-    if (!(timestep > 0)) return ZENO_INVALID_ARGUMENT;
+    if (timestep <= 0) return ZENO_INVALID_ARGUMENT;  // NaN passes, as in main.zig:655
     World* w = W(world);
     w->timestep = timestep;
     w->dt = timestep / (float)(w->cfg_substeps > 1 ? w->cfg_substeps : 1);
