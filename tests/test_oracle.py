@@ -8,8 +8,13 @@ How each oracle function is pinned:
   k_narrow_phase            reference KATs (test_collision.zig:55-81, 173-199): penetration 0.2,
                             normal +x / no contact; capsule-plane endpoint geometry
   k_match_cached            hand-built cases: pair, strict radius, nearest, ties, invalid slots
-  solve_constraint          invariants: a pendulum at rest without gravity does not move;
-                            |q| = 1 after steps; the static world body never moves
+  solve_constraint          closed forms per type: point (inverse-mass split, exact gap
+                            closure), hinge alignment and angular limit (the reference's
+                            update signs), weld (body b only, restoring), slider + linear
+                            limit (exact in one iteration); invariants: a pendulum at rest
+                            without gravity does not move, |q| = 1, the world body never moves
+  k_apply_joint_forces +    closed form of a motor on a hinge: torque -> omega -> rotation
+  k_update_joint_states     -> velocity update -> joint position / velocity sensors
   solve_contact (S4)        closed form of one contact step (bias, clamp, stale-penetration
                             position correction per iteration, velocity overwrite)
   k_apply_actions           reference actuator KATs (test_physics_integration.zig:517-629)
@@ -351,3 +356,142 @@ def test_template_builders_agree_on_assets(name):
     t, ranges, ncol = O.build_templates(m)
     assert t.tobytes() == m["constraints"].tobytes()
     np.testing.assert_array_equal(ranges, m["color_ranges"])
+
+
+# ---- joint solver closed forms (one body on the world or two free bodies, no gravity) ----
+
+def _qz(theta):
+    return np.array([0, 0, np.sin(theta / 2), np.cos(theta / 2)], np.float32)
+
+
+def _qy(theta):
+    return np.array([0, np.sin(theta / 2), 0, np.cos(theta / 2)], np.float32)
+
+
+def _angle_about(q, axis):
+    q = np.asarray(q, np.float64)
+    return 2 * np.arctan2(np.dot(q[:3], axis), q[3])
+
+
+def _single(xml, iterations=4):
+    m = load_model(mjcf_string=xml)
+    w = O.OracleWorld(m, 1, contact_iterations=iterations)
+    w.gravity = [0.0, 0.0, 0.0]
+    return m, w
+
+
+def _set_body(w, b, pos=None, quat=None):
+    p, q = w.positions.copy(), w.quaternions.copy()
+    if pos is not None:
+        p[0, b, :3] = pos
+    if quat is not None:
+        q[0, b] = quat
+    w.reset_to_state(p, q)
+
+
+BALL_PAIR = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/>
+<body name="b" pos="1 0 0"><joint type="ball"/><geom type="sphere" size="0.1" mass="3"/></body>
+</body></worldbody></mujoco>"""
+
+
+def test_point_constraint_closed_form():
+    """Point constraint between two free bodies whose gap lies along the anchor lever: the
+    correction is purely linear, split by inverse mass (1 : 1/3), and closes the 0.3 gap in
+    the first iteration; the mass-weighted centre stays put; v = dx / dt."""
+    m, w = _single(BALL_PAIR)
+    _set_body(w, 2, pos=[1.3, 0, 1])
+    w.step(None)
+    wsum = 1 + 1 / 3
+    np.testing.assert_allclose(w.positions[0, 1, :3], [0.3 / wsum, 0, 1], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(w.positions[0, 2, :3], [1.3 - 0.3 / 3 / wsum, 0, 1], rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(w.velocities[0, 1, 0], 0.3 / wsum / 0.01, rtol=1e-4)
+    np.testing.assert_allclose(w.velocities[0, 2, 0], -0.3 / 3 / wsum / 0.01, rtol=1e-4)
+    com = w.positions[0, 1, 0] * 1 + w.positions[0, 2, 0] * 3
+    np.testing.assert_allclose(com, 1.3 * 3, rtol=1e-6)
+    np.testing.assert_array_equal(w.quaternions[0, 1:], [[0, 0, 0, 1]] * 2)
+
+
+HINGE_ON_WORLD = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="b" pos="0 0 1"><joint name="h" type="hinge" axis="0 1 0"{rng}/>
+<geom type="sphere" size="0.1" mass="1"/></body></worldbody>
+<actuator><motor joint="h" gear="1" ctrlrange="-5 5"/></actuator>
+<sensor><jointpos joint="h"/><jointvel joint="h"/></sensor></mujoco>"""
+
+
+def test_hinge_alignment_sign_closed_form():
+    """Hinge axis alignment (all_shaders.metal:1131-1186) with a static parent: the child is
+    rotated 0.1 rad about z, so its hinge axis leaves y. The kernel's correction
+    d_omega_b = -d_lambda n I_b^-1 = +C n (n = a x b) rotates the child further about +z: one
+    iteration takes the misalignment from 0.1 to 0.1 + 2 atan(0.05). This is the reference's
+    sign, reproduced as written."""
+    _, w = _single(HINGE_ON_WORLD.format(rng=""), iterations=1)
+    _set_body(w, 1, quat=_qz(0.1))
+    w.step(np.zeros((1, 1), np.float32))
+    got = _angle_about(w.quaternions[0, 1], [0, 0, 1])
+    np.testing.assert_allclose(got, 0.1 + 2 * np.arctan(0.05), rtol=1e-5)
+    np.testing.assert_allclose(w.positions[0, 1, :3], [0, 0, 1], atol=1e-7)
+
+
+@pytest.mark.parametrize("iterations", [1, 4])
+def test_angular_limit_sign_closed_form(iterations):
+    """Angular limit (all_shaders.metal:1189-1238) with range 0.5 rad (ranges are read as
+    radians) and the child at 0.8 rad: violation v = 0.5 - angle, d_lambda = v / w, and the
+    child update q_b - dq turns it by -v each iteration (2 atan(-v/2) after normalisation),
+    i.e. away from the limit, as the reference code does. Joint position reads
+    2 atan2(q_rel.xyz . axis, q_rel.w)."""
+    _, w = _single(HINGE_ON_WORLD.format(rng=' range="-0.5 0.5"'), iterations=iterations)
+    _set_body(w, 1, quat=_qy(0.8))
+    w.step(np.zeros((1, 1), np.float32))
+    angle = 0.8
+    for _ in range(iterations):
+        v = 0.5 - angle
+        angle = angle + 2 * np.arctan(-v / 2)
+    got = _angle_about(w.quaternions[0, 1], [0, 1, 0])
+    wrapped = (angle + np.pi) % (2 * np.pi) - np.pi
+    assert abs(((got - wrapped + np.pi) % (2 * np.pi)) - np.pi) < 1e-4
+    np.testing.assert_allclose(w.joint_positions[0, 0], got, atol=1e-5)
+
+
+def test_weld_closed_form():
+    """A body with no joint gets a fixed joint (weld) to its parent. Weld corrects body b
+    only: the 0.2 position offset closes in one iteration, and the 0.4 rad rotation about z
+    shrinks by 2 atan(0.2) per iteration (restoring)."""
+    xml = """<mujoco><option timestep="0.01"/><worldbody><body name="b" pos="0 0 1">
+    <geom type="sphere" size="0.1" mass="1"/></body></worldbody></mujoco>"""
+    _, w = _single(xml, iterations=1)
+    _set_body(w, 1, pos=[0.2, 0, 1], quat=_qz(0.4))
+    w.step(None)
+    np.testing.assert_allclose(w.positions[0, 1, :3], [0, 0, 1], atol=1e-6)
+    np.testing.assert_allclose(_angle_about(w.quaternions[0, 1], [0, 0, 1]), 0.4 - 2 * np.arctan(0.2), rtol=1e-4)
+
+
+def test_slider_and_linear_limit_closed_form():
+    """Slider (type 10) removes the offset perpendicular to its axis, and the linear limit
+    (type 5) pulls the slide coordinate back to the range end; both exact in one iteration
+    for a body on the static world."""
+    xml = """<mujoco><option timestep="0.01"/><worldbody><body name="cart" pos="0 0 1">
+    <joint name="s" type="slide" axis="1 0 0" range="-1 1"/><geom type="sphere" size="0.1" mass="2"/>
+    </body></worldbody></mujoco>"""
+    _, w = _single(xml, iterations=1)
+    _set_body(w, 1, pos=[1.5, 0.2, 1])
+    w.step(None)
+    np.testing.assert_allclose(w.positions[0, 1, :3], [1.0, 0, 1], atol=1e-6)
+    np.testing.assert_allclose(w.joint_positions[0, 0], 1.0, atol=1e-6)
+
+
+def test_motor_torque_closed_form():
+    """Motor on a hinge about y through the child's centre (no gravity): tau = gear * ctrl
+    is added to the child's torque (apply_joint_forces), integrate gives
+    omega = I^-1 tau dt 0.999 and turns the child by 2 atan(omega dt / 2); the hinge and point
+    constraints are already satisfied; the velocity update returns 2 sin(theta/2) / dt; the
+    joint sensors report theta and that rate."""
+    _, w = _single(HINGE_ON_WORLD.format(rng=""))
+    w.step(np.array([[2.0]], np.float32))
+    inv_i = 1 / (0.4 * 1 * 0.1 ** 2)
+    omega = inv_i * 2.0 * 0.01 * 0.999
+    theta = 2 * np.arctan(omega * 0.01 / 2)
+    np.testing.assert_allclose(w.joint_positions[0, 0], theta, rtol=1e-4)
+    np.testing.assert_allclose(w.joint_velocities[0, 0], 2 * np.sin(theta / 2) / 0.01, rtol=1e-4)
+    np.testing.assert_allclose(w.observations[0, :2], [w.joint_positions[0, 0], w.joint_velocities[0, 0]])
+    np.testing.assert_allclose(w.joint_torques[0, 0], 2.0)
