@@ -56,7 +56,7 @@ __device__ __forceinline__ f3 qrot(f3 v, q4 q) {
 }
 __device__ __forceinline__ float qlen(q4 q) { return __builtin_sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w); }
 __device__ __forceinline__ q4 qnormalize(q4 q) {
-    float l = qlen(q);
+    const float l = qlen(q);
     return l > 1e-8f ? q4{q.x / l, q.y / l, q.z / l, q.w / l} : q4{0.0f, 0.0f, 0.0f, 1.0f};
 }
 // Quaternion step q + s * ((d, 0) (x) q) used by every XPBD rotation update.

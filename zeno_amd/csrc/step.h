@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstring>
+#include <vector>
+
 #include "layout.h"
 
 namespace za {
@@ -44,6 +47,93 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M) {
     return L;
 }
 
+// Joint-solve program. The colour-sorted constraint templates are re-packed on the host
+// into solve records whose fields are exactly what one constraint type reads, with the
+// static body data (inverse mass and inertia, centre of mass) already gathered, and into
+// phases: runs of one constraint type inside one colour. Constraints of a colour share no
+// body, so running a colour as several same-type phases gives the same result as any
+// order inside the colour, and every phase takes one branch for the whole wave.
+// Templates that the solver skips (types without a solver, or two static bodies) are
+// dropped here.
+constexpr uint32_t kJRecQuads = 7;  // float4 per solve record
+struct JointPhase { uint32_t type, start, count, pad; };
+
+// Record layout (float4 quads):
+//   q0 = (ia, ib, template index, flags: bit0 inv_m_a > 0, bit1 inv_m_b > 0)  [u32]
+//   q1 = inverse mass and inertia of body a, q2 = of body b
+//   q3.w = compliance (replaced by compliance / dt^2 in LDS at kernel start)
+//   POSITIONAL: q3.xyz anchor_a, q4.xyz anchor_b, q5.xyz com_a, q6.xyz com_b
+//   WELD:       q3.xyz anchor_a, q4.xyz anchor_b, q5 target quaternion
+//   ANGULAR:    q3.xyz axis_a, q4.xyz axis_b
+//   ANG. LIMIT: q3.xyz axis, q4.xy (lower, upper)
+//   LIN. LIMIT: q3.xyz axis, q4.xyz anchor_b, q5.xy (lower, upper)
+//   SLIDER:     q3.xyz anchor_a, q4.xyz anchor_b, q5.xyz axis, q6 target quaternion
+inline bool joint_type_solved(uint32_t t) {
+    return t == C_POSITIONAL || t == C_ANGULAR || t == C_ANGULAR_LIMIT || t == C_LINEAR_LIMIT || t == C_WELD ||
+           t == C_SLIDER;
+}
+
+inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const std::vector<uint32_t>& ranges,
+                                const float* invmi /* [B][4] */, const float* com /* [B][4] */,
+                                std::vector<float4>& recs, std::vector<JointPhase>& phases) {
+    recs.clear();
+    phases.clear();
+    const uint32_t ncol = (uint32_t)(ranges.size() / 2);
+    static const uint32_t order[] = {C_POSITIONAL, C_WELD, C_ANGULAR, C_ANGULAR_LIMIT, C_LINEAR_LIMIT, C_SLIDER};
+    auto u = [](uint32_t x) { float f; std::memcpy(&f, &x, 4); return f; };
+    for (uint32_t c = 0; c < ncol; ++c) {
+        const uint32_t off = ranges[2 * c], cnt = ranges[2 * c + 1];
+        for (uint32_t type : order) {
+            JointPhase ph{type, (uint32_t)(recs.size() / kJRecQuads), 0u, 0u};
+            for (uint32_t k = off; k < off + cnt; ++k) {
+                const ConstraintRec& t = tmpl[k];
+                if ((t.indices[3] & 0xFFu) != type) continue;
+                const uint32_t ia = t.indices[0], ib = t.indices[1];
+                const float* ma = invmi + 4 * ia;
+                const float* mb = invmi + 4 * ib;
+                if (ma[0] + mb[0] < 1e-8f) continue;  // all_shaders.metal:924: nothing to move
+                float4 q[kJRecQuads];
+                for (auto& x : q) x = make_float4(0, 0, 0, 0);
+                q[0] = make_float4(u(ia), u(ib), u(k), u((ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u)));
+                q[1] = make_float4(ma[0], ma[1], ma[2], ma[3]);
+                q[2] = make_float4(mb[0], mb[1], mb[2], mb[3]);
+                const float* A = t.anchor_a;
+                const float* Bv = t.anchor_b;
+                q[3] = make_float4(A[0], A[1], A[2], A[3]);
+                switch (type) {
+                    case C_POSITIONAL:
+                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                        q[5] = make_float4(com[4 * ia], com[4 * ia + 1], com[4 * ia + 2], 0);
+                        q[6] = make_float4(com[4 * ib], com[4 * ib + 1], com[4 * ib + 2], 0);
+                        break;
+                    case C_WELD:
+                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                        q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], t.axis_target[3]);
+                        break;
+                    case C_ANGULAR:
+                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                        break;
+                    case C_ANGULAR_LIMIT:
+                        q[4] = make_float4(t.limits[0], t.limits[1], 0, 0);
+                        break;
+                    case C_LINEAR_LIMIT:
+                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                        q[5] = make_float4(t.limits[0], t.limits[1], 0, 0);
+                        break;
+                    case C_SLIDER:
+                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                        q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], 0);
+                        q[6] = make_float4(t.limits[0], t.limits[1], t.limits[2], t.limits[3]);
+                        break;
+                }
+                recs.insert(recs.end(), q, q + kJRecQuads);
+                ++ph.count;
+            }
+            if (ph.count) phases.push_back(ph);
+        }
+    }
+}
+
 // Byte offsets of the per-scene model records inside the model blob. The blob is uploaded
 // once per world and copied into the front of every workgroup's LDS at kernel start, so
 // the solver phases never wait on global memory for model data.
@@ -54,26 +144,27 @@ struct ModelLayout {
     uint32_t pairs;              // u32[P]
     uint32_t acts;               // ActuatorRec[A]
     uint32_t sensors;            // SensorRec[S]
-    uint32_t tmpl;               // ConstraintRec[N]
-    uint32_t ranges;             // u32[2 * ncolors]
+    uint32_t jrec;               // float4[kJRecQuads * R] joint solve records
+    uint32_t jphase;             // JointPhase[nph]
     uint32_t bytes;              // total, multiple of 16
 };
 
 inline ModelLayout make_model_layout(uint32_t B, uint32_t J, uint32_t G, uint32_t P, uint32_t A, uint32_t S,
-                                     uint32_t N, uint32_t ncolors) {
+                                     uint32_t nrec, uint32_t nph) {
     ModelLayout L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
     L.invmi = take(16 * B); L.com = take(16 * B); L.flags = take(4 * B);
     L.joints = take(80 * J); L.geoms = take(64 * G); L.pairs = take(4 * P);
-    L.acts = take(32 * A); L.sensors = take(32 * S); L.tmpl = take(96 * N); L.ranges = take(8 * ncolors);
+    L.acts = take(32 * A); L.sensors = take(32 * S);
+    L.jrec = take(16 * kJRecQuads * nrec); L.jphase = take(16 * nph);
     L.bytes = o;
     return L;
 }
 
 struct StepArgs {
     // Sizes.
-    uint32_t E, B, J, Jp, A, S, obsp, N, ncolors, M, P;
+    uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P;
     uint32_t iters, substeps;
     // Scalars (SimParams, world.zig:35-56).
     float dt, inv_step, gx, gy, gz, restitution, baumgarte, slop;

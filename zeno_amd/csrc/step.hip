@@ -74,8 +74,8 @@ struct Mdl {
     const uint32_t* pairs;
     const ActuatorRec* acts;
     const SensorRec* sensors;
-    const ConstraintRec* tmpl;
-    const uint32_t* ranges;
+    const float4* jrec;
+    const JointPhase* jph;
 };
 
 __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const ModelLayout& L) {
@@ -88,199 +88,277 @@ __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const Model
     m.pairs = (const uint32_t*)(base + L.pairs);
     m.acts = (const ActuatorRec*)(base + L.acts);
     m.sensors = (const SensorRec*)(base + L.sensors);
-    m.tmpl = (const ConstraintRec*)(base + L.tmpl);
-    m.ranges = (const uint32_t*)(base + L.ranges);
+    m.jrec = (const float4*)(base + L.jrec);
+    m.jph = (const JointPhase*)(base + L.jphase);
     return m;
 }
 
 __device__ __forceinline__ void set_xyz(float4* p, f3 v) { p->x = v.x; p->y = v.y; p->z = v.z; }
 
 // ---------------------------------------------------------------------------------------
-// solve_joints, all_shaders.metal:909-1399, one constraint against LDS body state.
+// solve_joints, all_shaders.metal:909-1399: one constraint per lane, read from its solve
+// record (see build_joint_program), against LDS body state. One function per type.
 // ---------------------------------------------------------------------------------------
-__device__ void solve_constraint(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t ci) {
-    const ConstraintRec& c = md.tmpl[ci];
-    const uint32_t type = c.indices[3] & 0xFFu;
-    if (type > 10) return;
-    const uint32_t ia = c.indices[0], ib = c.indices[1];
-    const float4 imi_a = md.invmi[ia], imi_b = md.invmi[ib];
-    const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
-    const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
-    if (inv_mass_a + inv_mass_b < 1e-8f) return;
-    float4* Pa = &s.pos[ia];
-    float4* Pb = &s.pos[ib];
-    float4* Qa = &s.quat[ia];
-    float4* Qb = &s.quat[ib];
-    const f3 pos_a = xyz(*Pa), pos_b = xyz(*Pb);
-    const q4 quat_a = toq(*Qa), quat_b = toq(*Qb);
-    const float dt = a.dt;
-    const float alpha_tilde = c.anchor_a[3] / (dt * dt);
+__device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
 
-    if (type == C_POSITIONAL) {
-        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
-        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
-        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
-        float C = len(diff);
-        if (C > 1e-6f) {
-            f3 n = divs(diff, C);
-            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
-            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
-            float lambda_prev = s.lam[ci];
-            float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
-            s.lam[ci] = lambda_prev + d_lambda;
-            f3 impulse = sscale(d_lambda, n);
-            f3 rc_a = sub(r_a, qrot(xyz(md.com[ia]), quat_a));
-            f3 rc_b = sub(r_b, qrot(xyz(md.com[ib]), quat_b));
-            if (inv_mass_a > 0) {
-                set_xyz(Pa, add(xyz(*Pa), scale(impulse, inv_mass_a)));
-                *Qa = tof4(qnormalize(qadd(quat_a, qdelta(mul(cross(rc_a, impulse), iI_a), quat_a))));
-            }
-            if (inv_mass_b > 0) {
-                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
-                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(rc_b, impulse), iI_b), quat_b))));
-            }
-        }
-    } else if (type == C_WELD) {
-        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
-        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
-        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
-        float C = len(diff);
-        if (C > 1e-6f) {
-            f3 n = divs(diff, C);
-            f3 rn_b = cross(r_b, n);
-            float w_b = inv_mass_b + dot(mul(rn_b, iI_b), rn_b);
-            if (w_b > 1e-8f) {
-                float d_lambda = (-C) / (w_b + alpha_tilde);
-                f3 impulse = sscale(d_lambda, n);
-                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
-                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b))));
-            }
-        }
-        q4 target = mk4(c.axis_target[0], c.axis_target[1], c.axis_target[2], c.axis_target[3]);
-        q4 qa = toq(*Qa), qb = toq(*Qb);
-        q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
-        if (q_err.w < 0) q_err = qneg(q_err);
-        f3 e = xyz(q_err);
-        float sh = len(e);
-        if (sh > 1e-6f) {
-            f3 axis_rel = divs(e, sh);
-            float angle = 2.0f * z_atan2f(sh, q_err.w);
-            f3 aw = qrot(axis_rel, qa);
-            float w_b = dot(mul(aw, iI_b), aw);
-            if (w_b > 1e-8f) {
-                float d_lambda_ang = angle / (w_b + alpha_tilde);
-                f3 ang_impulse = sscale(d_lambda_ang, aw);
-                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
-            }
-        }
-    } else if (type == C_ANGULAR) {
-        q4 qa = toq(*Qa), qb = toq(*Qb);
-        f3 axa = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), qa);
-        f3 axb = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), qb);
-        f3 cr = cross(axa, axb);
-        float sin_angle = len(cr);
-        if (sin_angle > 1e-6f) {
-            f3 n = divs(cr, sin_angle);
-            float ang_C = z_asinf(clampf(sin_angle, -1.0f, 1.0f));
-            float w = dot(mul(n, iI_a), n) + dot(mul(n, iI_b), n);
-            if (w > 1e-8f) {
-                float d_lambda = -ang_C / (w + alpha_tilde);
-                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(sscale(d_lambda, n), iI_a), qa))));
-                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qadd(qb, qdelta(mul(sscale(-d_lambda, n), iI_b), qb))));
-            }
-        }
-    } else if (type == C_ANGULAR_LIMIT) {
-        f3 axis_local = mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]);
-        float lower = c.limits[0], upper = c.limits[1];
-        q4 qa = toq(*Qa), qb = toq(*Qb);
-        q4 q_rel = qmul(qconj(qa), qb);
-        float angle = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
-        float violation = 0.0f;
-        if (angle < lower) violation = lower - angle;
-        else if (angle > upper) violation = upper - angle;
-        if (__builtin_fabsf(violation) > 1e-6f) {
-            f3 aw = qrot(axis_local, qa);
-            float w = dot(mul(aw, iI_a), aw) + dot(mul(aw, iI_b), aw);
-            if (w > 1e-8f) {
-                float d_lambda = violation / (w + alpha_tilde);
-                f3 ang_impulse = sscale(d_lambda, aw);
-                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(ang_impulse, iI_a), qa))));
-                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
-            }
-        }
-    } else if (type == C_LINEAR_LIMIT) {
-        f3 axis_local = mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]);
-        float lower = c.limits[0], upper = c.limits[1];
-        q4 qa = toq(*Qa), qb = toq(*Qb);
-        f3 r_a = qrot(mk3(0.0f, 0.0f, 0.0f), qa);
-        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), qb);
-        f3 aw = qrot(axis_local, qa);
-        float dist = dot(sub(add(pos_b, r_b), add(pos_a, r_a)), aw);
-        float violation = 0.0f;
-        if (dist < lower) violation = lower - dist;
-        else if (dist > upper) violation = upper - dist;
-        if (__builtin_fabsf(violation) > 1e-6f) {
-            f3 n = violation > 0 ? aw : neg(aw);
-            float abs_v = __builtin_fabsf(violation);
-            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
-            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
-            if (w > 1e-8f) {
-                float d_lambda = abs_v / (w + alpha_tilde);
-                f3 impulse = sscale(d_lambda, n);
-                if (inv_mass_a > 0) set_xyz(Pa, sub(xyz(*Pa), scale(impulse, inv_mass_a)));
-                if (inv_mass_b > 0) set_xyz(Pb, add(xyz(*Pb), scale(impulse, inv_mass_b)));
-            }
-        }
-    } else if (type == C_SLIDER) {
-        f3 r_a = qrot(mk3(c.anchor_a[0], c.anchor_a[1], c.anchor_a[2]), quat_a);
-        f3 r_b = qrot(mk3(c.anchor_b[0], c.anchor_b[1], c.anchor_b[2]), quat_b);
-        f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
-        f3 aw = qrot(mk3(c.axis_target[0], c.axis_target[1], c.axis_target[2]), quat_a);
-        float along = dot(diff, aw);
-        f3 perp = sub(diff, sscale(along, aw));
-        float perp_len = len(perp);
-        if (perp_len > 1e-6f) {
-            f3 n = divs(perp, perp_len);
-            f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
-            float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
-            float d_lambda = (-perp_len) / (w + alpha_tilde);
-            f3 impulse = sscale(d_lambda, n);
-            if (inv_mass_a > 0) {
-                set_xyz(Pa, add(xyz(*Pa), scale(impulse, inv_mass_a)));
-                *Qa = tof4(qnormalize(qadd(quat_a, qdelta(mul(cross(r_a, impulse), iI_a), quat_a))));
-            }
-            if (inv_mass_b > 0) {
-                set_xyz(Pb, sub(xyz(*Pb), scale(impulse, inv_mass_b)));
-                *Qb = tof4(qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b))));
-            }
-        }
-        q4 target = mk4(c.limits[0], c.limits[1], c.limits[2], c.limits[3]);
-        q4 qa = toq(*Qa), qb = toq(*Qb);
-        q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
-        if (q_err.w < 0) q_err = qneg(q_err);
-        f3 e = xyz(q_err);
-        float sh = len(e);
-        if (sh > 1e-6f) {
-            f3 axis_err = divs(e, sh);
-            float angle_err = 2.0f * z_atan2f(sh, q_err.w);
-            f3 aw2 = qrot(axis_err, qa);
-            float w = dot(mul(aw2, iI_a), aw2) + dot(mul(aw2, iI_b), aw2);
-            if (w > 1e-8f) {
-                float d_lambda_ang = angle_err / (w + alpha_tilde);
-                f3 ang_impulse = sscale(d_lambda_ang, aw2);
-                if (inv_mass_a > 0) *Qa = tof4(qnormalize(qadd(qa, qdelta(mul(ang_impulse, iI_a), qa))));
-                if (inv_mass_b > 0) *Qb = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
-            }
+// Single-wave workgroups: LDS operations of one wave complete in program order, so a
+// compiler-level ordering point is all that is needed between dependent phases.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Lane pairs. The positional, hinge and angular-limit solves run on two adjacent lanes:
+// the even lane owns body a and the odd lane body b. Each lane evaluates the terms of its
+// own body (anchor rotation, generalized inverse mass term, position and orientation
+// update) and takes the partner's terms through a DPP swap, so one instruction stream
+// covers both bodies. Shared quantities (the constraint error, its direction, the
+// multiplier) are evaluated identically on both lanes, operands in the reference's order;
+// where the reference subtracts body b's update (x - d) the odd lane adds (-1 * d), which
+// is the same IEEE result.
+__device__ __forceinline__ float pair_swap(float v) {
+    // quad_perm(1, 0, 3, 2): exchange with the adjacent lane.
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ f3 pair_swap(f3 v) { return {pair_swap(v.x), pair_swap(v.y), pair_swap(v.z)}; }
+__device__ __forceinline__ q4 pair_swap(q4 v) { return {pair_swap(v.x), pair_swap(v.y), pair_swap(v.z), pair_swap(v.w)}; }
+__device__ __forceinline__ f3 sel(bool c, f3 x, f3 y) { return c ? x : y; }
+__device__ __forceinline__ q4 sel(bool c, q4 x, q4 y) { return c ? x : y; }
+__device__ __forceinline__ f3 signed3(float sg, f3 v) { return {sg * v.x, sg * v.y, sg * v.z}; }
+__device__ __forceinline__ q4 signed4(float sg, q4 v) { return {sg * v.x, sg * v.y, sg * v.z, sg * v.w}; }
+
+// :934-1037 positional (point-to-point), lane pair.
+__device__ __forceinline__ void solve_positional2(const float4* r, const Lds& s, bool odd) {
+    const float4 q0 = r[0];
+    const uint32_t ia = fbits(q0.x), ib = fbits(q0.y), ci = fbits(q0.z);
+    const uint32_t me = odd ? ib : ia;
+    const float4 mi = odd ? r[2] : r[1];
+    const float4 anc = odd ? r[4] : r[3];
+    const float4 com = odd ? r[6] : r[5];
+    const float alpha_tilde = r[3].w;
+    const float inv_mass = mi.x;
+    const f3 iI = mk3(mi.y, mi.z, mi.w);
+    const float sg = odd ? -1.0f : 1.0f;
+    const f3 P = xyz(s.pos[me]);
+    const q4 Q = toq(s.quat[me]);
+    const f3 rr = qrot(xyz(anc), Q);                       // r_a or r_b
+    const f3 u = add(P, rr);                               // pos + r
+    const f3 uo = pair_swap(u);
+    const f3 diff = sub(sel(odd, uo, u), sel(odd, u, uo));  // (pos_a + r_a) - (pos_b + r_b)
+    const float C = len(diff);
+    if (C > 1e-6f) {
+        const f3 n = divs(diff, C);
+        const f3 rn = cross(rr, n);
+        const float t = inv_mass + dot(mul(rn, iI), rn);
+        const float w = t + pair_swap(t);                  // (w_a) + (w_b), addition commutes
+        const float lambda_prev = s.lam[ci];
+        const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
+        if (!odd) s.lam[ci] = lambda_prev + d_lambda;
+        const f3 impulse = sscale(d_lambda, n);
+        const f3 rc = sub(rr, qrot(xyz(com), Q));
+        if (inv_mass > 0) {
+            set_xyz(&s.pos[me], add(P, signed3(sg, scale(impulse, inv_mass))));
+            s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(cross(rc, impulse), iI), Q)))));
         }
     }
+}
+
+// :1131-1186 hinge axis alignment, lane pair.
+__device__ __forceinline__ void solve_angular2(const float4* r, const Lds& s, bool odd) {
+    const float4 q0 = r[0];
+    const uint32_t me = odd ? fbits(q0.y) : fbits(q0.x);
+    const float4 mi = odd ? r[2] : r[1];
+    const float4 ax = odd ? r[4] : r[3];
+    const float alpha_tilde = r[3].w;
+    const float inv_mass = mi.x;
+    const f3 iI = mk3(mi.y, mi.z, mi.w);
+    const q4 Q = toq(s.quat[me]);
+    const f3 axw = qrot(xyz(ax), Q);
+    const f3 axo = pair_swap(axw);
+    const f3 cr = cross(sel(odd, axo, axw), sel(odd, axw, axo));
+    const float sin_angle = len(cr);
+    if (sin_angle > 1e-6f) {
+        const f3 n = divs(cr, sin_angle);
+        const float ang_C = z_asinf(clampf(sin_angle, -1.0f, 1.0f));
+        const float t = dot(mul(n, iI), n);
+        const float w = t + pair_swap(t);
+        if (w > 1e-8f) {
+            const float d_lambda = -ang_C / (w + alpha_tilde);
+            const float dl = odd ? -d_lambda : d_lambda;
+            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, qdelta(mul(sscale(dl, n), iI), Q))));
+        }
+    }
+}
+
+// :1189-1238 angular limit, lane pair.
+__device__ __forceinline__ void solve_angular_limit2(const float4* r, const Lds& s, bool odd) {
+    const float4 q0 = r[0], a3 = r[3], lim = r[4];
+    const uint32_t me = odd ? fbits(q0.y) : fbits(q0.x);
+    const float4 mi = odd ? r[2] : r[1];
+    const float alpha_tilde = a3.w;
+    const float inv_mass = mi.x;
+    const f3 iI = mk3(mi.y, mi.z, mi.w);
+    const float sg = odd ? -1.0f : 1.0f;
+    const f3 axis_local = xyz(a3);
+    const float lower = lim.x, upper = lim.y;
+    const q4 Q = toq(s.quat[me]);
+    const q4 Qo = pair_swap(Q);
+    const q4 qa = sel(odd, Qo, Q), qb = sel(odd, Q, Qo);
+    const q4 q_rel = qmul(qconj(qa), qb);
+    const float angle = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
+    float violation = 0.0f;
+    if (angle < lower) violation = lower - angle;
+    else if (angle > upper) violation = upper - angle;
+    if (__builtin_fabsf(violation) > 1e-6f) {
+        const f3 aw = qrot(axis_local, qa);
+        const float t = dot(mul(aw, iI), aw);
+        const float w = t + pair_swap(t);
+        if (w > 1e-8f) {
+            const float d_lambda = violation / (w + alpha_tilde);
+            const f3 ang_impulse = sscale(d_lambda, aw);
+            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(ang_impulse, iI), Q)))));
+        }
+    }
+}
+
+// :1039-1129 weld (corrects body b only), one lane.
+__device__ __forceinline__ void solve_weld(const float4* r, const Lds& s) {
+    const float4 q0 = r[0], mb = r[2], a3 = r[3], b4 = r[4], tg = r[5];
+    const uint32_t ia = fbits(q0.x), ib = fbits(q0.y);
+    const float inv_mass_b = mb.x;
+    const f3 iI_b = mk3(mb.y, mb.z, mb.w);
+    const float alpha_tilde = a3.w;
+    const f3 pos_a = xyz(s.pos[ia]), pos_b = xyz(s.pos[ib]);
+    const q4 quat_a = toq(s.quat[ia]), quat_b = toq(s.quat[ib]);
+    f3 r_a = qrot(xyz(a3), quat_a);
+    f3 r_b = qrot(xyz(b4), quat_b);
+    f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
+    float C = len(diff);
+    q4 qb = quat_b;
+    if (C > 1e-6f) {
+        f3 n = divs(diff, C);
+        f3 rn_b = cross(r_b, n);
+        float w_b = inv_mass_b + dot(mul(rn_b, iI_b), rn_b);
+        if (w_b > 1e-8f) {
+            float d_lambda = (-C) / (w_b + alpha_tilde);
+            f3 impulse = sscale(d_lambda, n);
+            set_xyz(&s.pos[ib], sub(pos_b, scale(impulse, inv_mass_b)));
+            qb = qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b)));
+            s.quat[ib] = tof4(qb);
+        }
+    }
+    const q4 target = toq(tg);
+    const q4 qa = quat_a;
+    q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
+    if (q_err.w < 0) q_err = qneg(q_err);
+    f3 e = xyz(q_err);
+    float sh = len(e);
+    if (sh > 1e-6f) {
+        f3 axis_rel = divs(e, sh);
+        float angle = 2.0f * z_atan2f(sh, q_err.w);
+        f3 aw = qrot(axis_rel, qa);
+        float w_b = dot(mul(aw, iI_b), aw);
+        if (w_b > 1e-8f) {
+            float d_lambda_ang = angle / (w_b + alpha_tilde);
+            f3 ang_impulse = sscale(d_lambda_ang, aw);
+            if (inv_mass_b > 0) s.quat[ib] = tof4(qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb))));
+        }
+    }
+}
+
+// :1241-1293 linear limit, one lane.
+__device__ __forceinline__ void solve_linear_limit(const float4* r, const Lds& s) {
+    const float4 q0 = r[0], ma = r[1], mb = r[2], a3 = r[3], b4 = r[4], lim = r[5];
+    const uint32_t ia = fbits(q0.x), ib = fbits(q0.y);
+    const float inv_mass_a = ma.x, inv_mass_b = mb.x;
+    const f3 iI_a = mk3(ma.y, ma.z, ma.w), iI_b = mk3(mb.y, mb.z, mb.w);
+    const float alpha_tilde = a3.w;
+    const f3 axis_local = xyz(a3);
+    const float lower = lim.x, upper = lim.y;
+    const f3 pos_a = xyz(s.pos[ia]), pos_b = xyz(s.pos[ib]);
+    const q4 qa = toq(s.quat[ia]), qb = toq(s.quat[ib]);
+    f3 r_a = qrot(mk3(0.0f, 0.0f, 0.0f), qa);
+    f3 r_b = qrot(xyz(b4), qb);
+    f3 aw = qrot(axis_local, qa);
+    float dist = dot(sub(add(pos_b, r_b), add(pos_a, r_a)), aw);
+    float violation = 0.0f;
+    if (dist < lower) violation = lower - dist;
+    else if (dist > upper) violation = upper - dist;
+    if (__builtin_fabsf(violation) > 1e-6f) {
+        f3 n = violation > 0 ? aw : neg(aw);
+        float abs_v = __builtin_fabsf(violation);
+        f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
+        float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+        if (w > 1e-8f) {
+            float d_lambda = abs_v / (w + alpha_tilde);
+            f3 impulse = sscale(d_lambda, n);
+            if (inv_mass_a > 0) set_xyz(&s.pos[ia], sub(pos_a, scale(impulse, inv_mass_a)));
+            if (inv_mass_b > 0) set_xyz(&s.pos[ib], add(pos_b, scale(impulse, inv_mass_b)));
+        }
+    }
+}
+
+// :1296-1399 slider, one lane.
+__device__ __forceinline__ void solve_slider(const float4* r, const Lds& s) {
+    const float4 q0 = r[0], ma = r[1], mb = r[2], a3 = r[3], b4 = r[4], ax = r[5], tg = r[6];
+    const uint32_t ia = fbits(q0.x), ib = fbits(q0.y);
+    const float inv_mass_a = ma.x, inv_mass_b = mb.x;
+    const f3 iI_a = mk3(ma.y, ma.z, ma.w), iI_b = mk3(mb.y, mb.z, mb.w);
+    const float alpha_tilde = a3.w;
+    const f3 pos_a = xyz(s.pos[ia]), pos_b = xyz(s.pos[ib]);
+    const q4 quat_a = toq(s.quat[ia]), quat_b = toq(s.quat[ib]);
+    f3 r_a = qrot(xyz(a3), quat_a);
+    f3 r_b = qrot(xyz(b4), quat_b);
+    f3 diff = sub(add(pos_a, r_a), add(pos_b, r_b));
+    f3 aw = qrot(xyz(ax), quat_a);
+    float along = dot(diff, aw);
+    f3 perp = sub(diff, sscale(along, aw));
+    float perp_len = len(perp);
+    q4 qa = quat_a, qb = quat_b;
+    if (perp_len > 1e-6f) {
+        f3 n = divs(perp, perp_len);
+        f3 rn_a = cross(r_a, n), rn_b = cross(r_b, n);
+        float w = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+        float d_lambda = (-perp_len) / (w + alpha_tilde);
+        f3 impulse = sscale(d_lambda, n);
+        if (inv_mass_a > 0) {
+            set_xyz(&s.pos[ia], add(pos_a, scale(impulse, inv_mass_a)));
+            qa = qnormalize(qadd(quat_a, qdelta(mul(cross(r_a, impulse), iI_a), quat_a)));
+        }
+        if (inv_mass_b > 0) {
+            set_xyz(&s.pos[ib], sub(pos_b, scale(impulse, inv_mass_b)));
+            qb = qnormalize(qsub(quat_b, qdelta(mul(cross(r_b, impulse), iI_b), quat_b)));
+        }
+    }
+    const q4 target = toq(tg);
+    q4 q_err = qmul(qmul(qconj(qa), qb), qconj(target));
+    if (q_err.w < 0) q_err = qneg(q_err);
+    f3 e = xyz(q_err);
+    float sh = len(e);
+    if (sh > 1e-6f) {
+        f3 axis_err = divs(e, sh);
+        float angle_err = 2.0f * z_atan2f(sh, q_err.w);
+        f3 aw2 = qrot(axis_err, qa);
+        float w = dot(mul(aw2, iI_a), aw2) + dot(mul(aw2, iI_b), aw2);
+        if (w > 1e-8f) {
+            float d_lambda_ang = angle_err / (w + alpha_tilde);
+            f3 ang_impulse = sscale(d_lambda_ang, aw2);
+            if (inv_mass_a > 0) qa = qnormalize(qadd(qa, qdelta(mul(ang_impulse, iI_a), qa)));
+            if (inv_mass_b > 0) qb = qnormalize(qsub(qb, qdelta(mul(ang_impulse, iI_b), qb)));
+        }
+    }
+    if (inv_mass_a > 0) s.quat[ia] = tof4(qa);
+    if (inv_mass_b > 0) s.quat[ib] = tof4(qb);
 }
 
 // ---------------------------------------------------------------------------------------
 // solve_contacts, all_shaders.metal:1644-1793, one contact record.
 // ---------------------------------------------------------------------------------------
-__device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr) {
+__device__ __forceinline__ void contact_core(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr,
+                                             float4 Pa0, float4 Pb0, float4 Va0, float4 Vb0, float4 Wa0, float4 Wb0,
+                                             float j_prev) {
     const float4 pp = *(const float4*)cr->position_pen;
-    if (pp.w < 0) return;
     const float4 nf = *(const float4*)cr->normal_friction;
     const uint32_t ia = cr->indices[0], ib = cr->indices[1];
     const float4 imi_a = md.invmi[ia], imi_b = md.invmi[ib];
@@ -291,15 +369,10 @@ __device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, Co
     const f3 normal = mk3(nf.x, nf.y, nf.z);
     const float penetration = pp.w, friction = nf.w;
     const f3 cp = mk3(pp.x, pp.y, pp.z);
-    float4* Pa = &s.pos[ia];
-    float4* Pb = &s.pos[ib];
-    float4* Va = &s.vel[ia];
-    float4* Vb = &s.vel[ib];
-    float4* Wa = &s.angvel[ia];
-    float4* Wb = &s.angvel[ib];
-    const f3 r_a = sub(cp, xyz(*Pa)), r_b = sub(cp, xyz(*Pb));
-    const f3 vel_a = add(xyz(*Va), cross(xyz(*Wa), r_a));
-    const f3 vel_b = add(xyz(*Vb), cross(xyz(*Wb), r_b));
+    f3 va = xyz(Va0), vb = xyz(Vb0), wa = xyz(Wa0), wb = xyz(Wb0);
+    const f3 r_a = sub(cp, xyz(Pa0)), r_b = sub(cp, xyz(Pb0));
+    const f3 vel_a = add(va, cross(wa, r_a));
+    const f3 vel_b = add(vb, cross(wb, r_b));
     const f3 rel_vel = sub(vel_a, vel_b);
     const float vel_normal = dot(rel_vel, normal);
     const f3 vel_tangent = sub(rel_vel, sscale(vel_normal, normal));
@@ -315,18 +388,18 @@ __device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, Co
     const f3 impulse_n = sscale(j_n, normal);
     const float pos_correction = a.baumgarte * fmaxf(penetration - a.slop, 0.0f);
     if (inv_mass_a > 1e-8f) {
-        set_xyz(Va, add(xyz(*Va), scale(impulse_n, inv_mass_a)));
-        set_xyz(Wa, add(xyz(*Wa), mul(cross(r_a, impulse_n), iI_a)));
+        va = add(va, scale(impulse_n, inv_mass_a));
+        wa = add(wa, mul(cross(r_a, impulse_n), iI_a));
         float ratio = inv_mass_a / inv_mass_sum;
-        set_xyz(Pa, add(xyz(*Pa), sscale(pos_correction * ratio, normal)));
+        set_xyz(&s.pos[ia], add(xyz(Pa0), sscale(pos_correction * ratio, normal)));
     }
     if (inv_mass_b > 1e-8f) {
-        set_xyz(Vb, sub(xyz(*Vb), scale(impulse_n, inv_mass_b)));
-        set_xyz(Wb, sub(xyz(*Wb), mul(cross(r_b, impulse_n), iI_b)));
+        vb = sub(vb, scale(impulse_n, inv_mass_b));
+        wb = sub(wb, mul(cross(r_b, impulse_n), iI_b));
         float ratio = inv_mass_b / inv_mass_sum;
-        set_xyz(Pb, sub(xyz(*Pb), sscale(pos_correction * ratio, normal)));
+        set_xyz(&s.pos[ib], sub(xyz(Pb0), sscale(pos_correction * ratio, normal)));
     }
-    const float j_n_acc = cr->impulses[0] + j_n;
+    const float j_n_acc = j_prev + j_n;
     if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
         f3 tangent = divs(vel_tangent, tangent_speed);
         f3 rt_a = cross(r_a, tangent), rt_b = cross(r_b, tangent);
@@ -335,16 +408,24 @@ __device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, Co
             float j_t = fminf(tangent_speed / w_tangent, friction * j_n_acc);
             f3 impulse_t = sscale(j_t, tangent);
             if (inv_mass_a > 1e-8f) {
-                set_xyz(Va, sub(xyz(*Va), scale(impulse_t, inv_mass_a)));
-                set_xyz(Wa, sub(xyz(*Wa), mul(cross(r_a, impulse_t), iI_a)));
+                va = sub(va, scale(impulse_t, inv_mass_a));
+                wa = sub(wa, mul(cross(r_a, impulse_t), iI_a));
             }
             if (inv_mass_b > 1e-8f) {
-                set_xyz(Vb, add(xyz(*Vb), scale(impulse_t, inv_mass_b)));
-                set_xyz(Wb, add(xyz(*Wb), mul(cross(r_b, impulse_t), iI_b)));
+                vb = add(vb, scale(impulse_t, inv_mass_b));
+                wb = add(wb, mul(cross(r_b, impulse_t), iI_b));
             }
         }
     }
+    if (inv_mass_a > 1e-8f) { set_xyz(&s.vel[ia], va); set_xyz(&s.angvel[ia], wa); }
+    if (inv_mass_b > 1e-8f) { set_xyz(&s.vel[ib], vb); set_xyz(&s.angvel[ib], wb); }
     cr->impulses[0] = j_n;
+}
+
+__device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr) {
+    if (cr->position_pen[3] < 0) return;
+    const uint32_t ia = cr->indices[0], ib = cr->indices[1];
+    contact_core(a, md, s, cr, s.pos[ia], s.pos[ib], s.vel[ia], s.vel[ib], s.angvel[ia], s.angvel[ib], cr->impulses[0]);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -442,6 +523,13 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
 
     // ---- Model records (one blob per scene) -> LDS -------------------------------------
     for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
+    __syncthreads();
+    // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
+    // this launch: computed once per record.
+    for (uint32_t i = tid; i < a.nrec; i += kWave) {
+        float4* q3 = (float4*)(smem + a.ml.jrec) + i * kJRecQuads + 3;
+        q3->w = q3->w / (a.dt * a.dt);
+    }
 
     // ---- Load the env's working set (HBM -> LDS) --------------------------------------
     uint32_t count = 0, pcount = 0;
@@ -558,8 +646,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 q4 q = toq(s.quat[b]);
                 f3 h = scale(scale(om, a.dt), 0.5f);
                 q = qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q));
-                float ql = qlen(q);
-                q = ql > 1e-8f ? q4{q.x / ql, q.y / ql, q.z / ql, q.w / ql} : q4{0.0f, 0.0f, 0.0f, 1.0f};
+                q = qnormalize(q);
                 s.angvel[b] = tof4(om, 0.0f);
                 s.quat[b] = tof4(q);
             }
@@ -737,11 +824,31 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         tick(PH_NARROW);
         // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
+        // Phases are same-type runs inside a colour (build_joint_program); the type is
+        // uniform, so each phase takes one scalar branch.
         for (uint32_t it = 0; it < a.iters; ++it) {
-            for (uint32_t col = 0; col < a.ncolors; ++col) {
-                const uint32_t off = md.ranges[2 * col], cnt = md.ranges[2 * col + 1];
-                if (live) for (uint32_t k = sl; k < cnt; k += G) solve_constraint(a, md, s, off + k);
-                __syncthreads();
+            for (uint32_t p = 0; p < a.njph; ++p) {
+                const JointPhase ph = md.jph[p];
+                const uint32_t type = __builtin_amdgcn_readfirstlane(ph.type);
+                const uint32_t start = __builtin_amdgcn_readfirstlane(ph.start);
+                const uint32_t cnt = __builtin_amdgcn_readfirstlane(ph.count);
+                if (live) {
+                    // Lane pair (2k, 2k+1) of the env's lanes takes constraint k.
+                    const bool odd = (sl & 1) != 0;
+                    for (uint32_t k = sl >> 1; k < cnt; k += G / 2) {
+                        const float4* r = md.jrec + (start + k) * kJRecQuads;
+                        switch (type) {
+                            case C_POSITIONAL: solve_positional2(r, s, odd); break;
+                            case C_ANGULAR: solve_angular2(r, s, odd); break;
+                            case C_ANGULAR_LIMIT: solve_angular_limit2(r, s, odd); break;
+                            case C_WELD: if (!odd) solve_weld(r, s); break;
+                            case C_LINEAR_LIMIT: if (!odd) solve_linear_limit(r, s); break;
+                            case C_SLIDER: if (!odd) solve_slider(r, s); break;
+                            default: break;
+                        }
+                    }
+                }
+                wave_sync();
             }
         }
         tick(PH_JOINTS);

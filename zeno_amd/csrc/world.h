@@ -20,6 +20,7 @@ enum MirrorId {
 struct World {
     Model model;
     uint32_t E = 0, B = 0, J = 0, Jp = 1, A = 0, Ap = 1, obsp = 1, N = 0, M = 0;
+    uint32_t nrec = 0, njph = 0;  // joint solve records and phases
     uint32_t iters = 4, cfg_substeps = 1, adaptive_substeps = 1;
     uint64_t seed = 42;
     bool profiling = false;

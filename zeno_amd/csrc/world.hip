@@ -149,7 +149,20 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS.
     const EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1));
     w->lds = L;
-    const ModelLayout ML = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->N, m.num_colors);
+    std::vector<float4> invmi(w->B), com(w->B);
+    std::vector<uint32_t> flags(w->B);
+    for (uint32_t b = 0; b < w->B; ++b) {
+        const float* im = &m.inv_mass_inertia[4 * b];
+        invmi[b] = make_float4(im[0], im[1], im[2], im[3]);
+        com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
+        flags[b] = ((uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u) | (im[0] > 1e-8f ? 2u : 0u);
+    }
+    std::vector<float4> jrec;
+    std::vector<JointPhase> jph;
+    build_joint_program(m.templates, m.color_ranges, (const float*)invmi.data(), (const float*)com.data(), jrec, jph);
+    w->nrec = (uint32_t)(jrec.size() / kJRecQuads);
+    w->njph = (uint32_t)jph.size();
+    const ModelLayout ML = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->nrec, w->njph);
     int epw = 1;
     for (int cand : {8, 4, 2}) {
         if (w->M > max_contacts_for(cand)) continue;
@@ -173,18 +186,10 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
 
     // Model blob: every per-scene record the kernel reads, packed per ModelLayout.
-    w->ml = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->N, m.num_colors);
+    w->ml = ML;
     {
         std::vector<unsigned char> blob(w->ml.bytes, 0);
         auto put = [&](uint32_t off, const void* src, size_t bytes) { if (bytes) std::memcpy(blob.data() + off, src, bytes); };
-        std::vector<float4> invmi(w->B), com(w->B);
-        std::vector<uint32_t> flags(w->B);
-        for (uint32_t b = 0; b < w->B; ++b) {
-            const float* im = &m.inv_mass_inertia[4 * b];
-            invmi[b] = make_float4(im[0], im[1], im[2], im[3]);
-            com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
-            flags[b] = ((uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u) | (im[0] > 1e-8f ? 2u : 0u);
-        }
         put(w->ml.invmi, invmi.data(), 16 * w->B);
         put(w->ml.com, com.data(), 16 * w->B);
         put(w->ml.flags, flags.data(), 4 * w->B);
@@ -193,8 +198,8 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         put(w->ml.pairs, m.pairs.data(), 4 * m.pairs.size());
         put(w->ml.acts, m.actuators.data(), sizeof(ActuatorRec) * m.actuators.size());
         put(w->ml.sensors, m.sensors.data(), sizeof(SensorRec) * m.sensors.size());
-        put(w->ml.tmpl, m.templates.data(), sizeof(ConstraintRec) * m.templates.size());
-        put(w->ml.ranges, m.color_ranges.data(), 4 * m.color_ranges.size());
+        put(w->ml.jrec, jrec.data(), sizeof(float4) * jrec.size());
+        put(w->ml.jphase, jph.data(), sizeof(JointPhase) * jph.size());
         if ((e = upload(w, &w->d_model, (const uint4*)blob.data(), w->ml.bytes / 16)) != hipSuccess) return fail("upload", e);
     }
     std::vector<float4> ip(w->B), iq(w->B), iv(w->B), ia(w->B);
@@ -272,7 +277,7 @@ uint64_t World::state_bytes() const { return device_bytes; }
 hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask) {
     StepArgs a{};
     a.E = E; a.B = B; a.J = J; a.Jp = Jp; a.A = A; a.S = model.num_sensors; a.obsp = obsp; a.N = N;
-    a.ncolors = model.num_colors; a.M = M; a.P = model.num_pairs;
+    a.nrec = nrec; a.njph = njph; a.M = M; a.P = model.num_pairs;
     a.iters = iters; a.substeps = substeps;
     a.dt = dt;
     a.inv_step = timestep > 0 ? 1.0f / timestep : 0.0f;
