@@ -17,9 +17,13 @@ struct EnvLds {
     uint32_t lam;                                                      // float[N]
     uint32_t con;                                                      // ContactRec[M] (physical)
     uint32_t perm;                                                     // u16[M] logical -> physical
-    uint32_t skey;                                                     // u32[M] sort keys / levels
-    uint32_t pkey, ppen, pimp;                                         // prev: u32[M], float4[M], float4[M]
-    uint32_t order;                                                    // u16[M] contact levels
+    uint32_t skey;                                                     // u32[M] sort keys
+    uint32_t ppen, pimp;                                               // prev snapshot: float4[M] x2
+    uint32_t order;                                                    // u16[M] level of each valid slot
+    // Contact schedule, aliased onto arrays that are dead by then: vlist and lst (u16[M]
+    // each: valid slots, valid slots by level) share skey; loff (u16[M + 2], level ranges
+    // in lst) shares ppen.
+    uint32_t vlist, lst, loff;
     uint32_t last;                                                     // u16[B]
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
     uint32_t bytes;                                                    // total, multiple of 16
@@ -39,8 +43,10 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M) {
     L.con = take(64 * M);
     L.perm = take(2 * M);
     L.skey = take(4 * M);
-    L.pkey = take(4 * M); L.ppen = take(16 * M); L.pimp = take(16 * M);
+    L.ppen = take(16 * M); L.pimp = take(16 * M);
     L.order = take(2 * M);
+    L.vlist = L.skey; L.lst = L.skey + 2 * M;
+    L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
     L.last = take(2 * B);
     L.misc = take(16);
     L.bytes = o;

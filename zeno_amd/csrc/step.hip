@@ -38,9 +38,8 @@ struct Lds {
     ContactRec* con;
     uint16_t* perm;
     uint32_t* skey;
-    uint32_t* pkey;
-    float4 *ppen, *pimp;
-    uint16_t *order, *last;
+    float4 *ppen, *pimp;  // prev snapshot: position_pen; impulses.xyz with the pair key in .w
+    uint16_t *order, *vlist, *lst, *loff, *last;
     uint32_t* misc;
 };
 
@@ -56,9 +55,11 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.con = (ContactRec*)(base + L.con);
     s.perm = (uint16_t*)(base + L.perm);
     s.skey = (uint32_t*)(base + L.skey);
-    s.pkey = (uint32_t*)(base + L.pkey);
     s.ppen = (float4*)(base + L.ppen); s.pimp = (float4*)(base + L.pimp);
     s.order = (uint16_t*)(base + L.order);
+    s.vlist = (uint16_t*)(base + L.vlist);
+    s.lst = (uint16_t*)(base + L.lst);
+    s.loff = (uint16_t*)(base + L.loff);
     s.last = (uint16_t*)(base + L.last);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
@@ -353,32 +354,38 @@ __device__ __forceinline__ void solve_slider(const float4* r, const Lds& s) {
 }
 
 // ---------------------------------------------------------------------------------------
-// solve_contacts, all_shaders.metal:1644-1793, one contact record.
+// solve_contacts, all_shaders.metal:1644-1793.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void contact_core(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr,
-                                             float4 Pa0, float4 Pb0, float4 Va0, float4 Vb0, float4 Wa0, float4 Wb0,
-                                             float j_prev) {
+// solve_contacts on a lane pair: the even lane owns body a, the odd lane body b (see the
+// joint lane pairs). Operands keep the reference's order; body b's updates, which the
+// reference subtracts, are added with a factor of -1.
+__device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr,
+                                               bool odd) {
     const float4 pp = *(const float4*)cr->position_pen;
     const float4 nf = *(const float4*)cr->normal_friction;
     const uint32_t ia = cr->indices[0], ib = cr->indices[1];
-    const float4 imi_a = md.invmi[ia], imi_b = md.invmi[ib];
-    const float inv_mass_a = imi_a.x, inv_mass_b = imi_b.x;
-    const f3 iI_a = mk3(imi_a.y, imi_a.z, imi_a.w), iI_b = mk3(imi_b.y, imi_b.z, imi_b.w);
-    const float inv_mass_sum = inv_mass_a + inv_mass_b;
+    const uint32_t me = odd ? ib : ia;
+    const float4 imi = md.invmi[me];
+    const float inv_mass = imi.x;
+    const f3 iI = mk3(imi.y, imi.z, imi.w);
+    const float inv_mass_o = pair_swap(inv_mass);
+    const float inv_mass_sum = odd ? inv_mass_o + inv_mass : inv_mass + inv_mass_o;
     if (inv_mass_sum < 1e-8f) return;
     const f3 normal = mk3(nf.x, nf.y, nf.z);
     const float penetration = pp.w, friction = nf.w;
     const f3 cp = mk3(pp.x, pp.y, pp.z);
-    f3 va = xyz(Va0), vb = xyz(Vb0), wa = xyz(Wa0), wb = xyz(Wb0);
-    const f3 r_a = sub(cp, xyz(Pa0)), r_b = sub(cp, xyz(Pb0));
-    const f3 vel_a = add(va, cross(wa, r_a));
-    const f3 vel_b = add(vb, cross(wb, r_b));
-    const f3 rel_vel = sub(vel_a, vel_b);
+    const float4 P0 = s.pos[me], V0 = s.vel[me], W0 = s.angvel[me];
+    const float sg = odd ? -1.0f : 1.0f;
+    const f3 r = sub(cp, xyz(P0));
+    const f3 vpt = add(xyz(V0), cross(xyz(W0), r));
+    const f3 vpo = pair_swap(vpt);
+    const f3 rel_vel = sub(sel(odd, vpo, vpt), sel(odd, vpt, vpo));
     const float vel_normal = dot(rel_vel, normal);
     const f3 vel_tangent = sub(rel_vel, sscale(vel_normal, normal));
     const float tangent_speed = len(vel_tangent);
-    const f3 rn_a = cross(r_a, normal), rn_b = cross(r_b, normal);
-    const float w_normal = (inv_mass_a + dot(mul(rn_a, iI_a), rn_a)) + (inv_mass_b + dot(mul(rn_b, iI_b), rn_b));
+    const f3 rn = cross(r, normal);
+    const float tn = inv_mass + dot(mul(rn, iI), rn);
+    const float w_normal = tn + pair_swap(tn);
     if (w_normal < 1e-8f) return;
     const float bias = a.baumgarte * fmaxf(penetration - a.slop, 0.0f) / a.dt;
     const float restitution = cr->impulses[3];
@@ -387,45 +394,33 @@ __device__ __forceinline__ void contact_core(const StepArgs& a, const Mdl& md, c
     j_n = fmaxf(j_n, 0.0f);
     const f3 impulse_n = sscale(j_n, normal);
     const float pos_correction = a.baumgarte * fmaxf(penetration - a.slop, 0.0f);
-    if (inv_mass_a > 1e-8f) {
-        va = add(va, scale(impulse_n, inv_mass_a));
-        wa = add(wa, mul(cross(r_a, impulse_n), iI_a));
-        float ratio = inv_mass_a / inv_mass_sum;
-        set_xyz(&s.pos[ia], add(xyz(Pa0), sscale(pos_correction * ratio, normal)));
+    f3 v = xyz(V0), w = xyz(W0);
+    if (inv_mass > 1e-8f) {
+        v = add(v, signed3(sg, scale(impulse_n, inv_mass)));
+        w = add(w, signed3(sg, mul(cross(r, impulse_n), iI)));
+        const float ratio = inv_mass / inv_mass_sum;
+        set_xyz(&s.pos[me], add(xyz(P0), signed3(sg, sscale(pos_correction * ratio, normal))));
     }
-    if (inv_mass_b > 1e-8f) {
-        vb = sub(vb, scale(impulse_n, inv_mass_b));
-        wb = sub(wb, mul(cross(r_b, impulse_n), iI_b));
-        float ratio = inv_mass_b / inv_mass_sum;
-        set_xyz(&s.pos[ib], sub(xyz(Pb0), sscale(pos_correction * ratio, normal)));
-    }
-    const float j_n_acc = j_prev + j_n;
+    const float j_n_acc = cr->impulses[0] + j_n;
     if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
-        f3 tangent = divs(vel_tangent, tangent_speed);
-        f3 rt_a = cross(r_a, tangent), rt_b = cross(r_b, tangent);
-        float w_tangent = (inv_mass_a + dot(mul(rt_a, iI_a), rt_a)) + (inv_mass_b + dot(mul(rt_b, iI_b), rt_b));
+        const f3 tangent = divs(vel_tangent, tangent_speed);
+        const f3 rt = cross(r, tangent);
+        const float tt = inv_mass + dot(mul(rt, iI), rt);
+        const float w_tangent = tt + pair_swap(tt);
         if (w_tangent > 1e-8f) {
-            float j_t = fminf(tangent_speed / w_tangent, friction * j_n_acc);
-            f3 impulse_t = sscale(j_t, tangent);
-            if (inv_mass_a > 1e-8f) {
-                va = sub(va, scale(impulse_t, inv_mass_a));
-                wa = sub(wa, mul(cross(r_a, impulse_t), iI_a));
-            }
-            if (inv_mass_b > 1e-8f) {
-                vb = add(vb, scale(impulse_t, inv_mass_b));
-                wb = add(wb, mul(cross(r_b, impulse_t), iI_b));
+            const float j_t = fminf(tangent_speed / w_tangent, friction * j_n_acc);
+            const f3 impulse_t = sscale(j_t, tangent);
+            if (inv_mass > 1e-8f) {
+                v = add(v, signed3(-sg, scale(impulse_t, inv_mass)));
+                w = add(w, signed3(-sg, mul(cross(r, impulse_t), iI)));
             }
         }
     }
-    if (inv_mass_a > 1e-8f) { set_xyz(&s.vel[ia], va); set_xyz(&s.angvel[ia], wa); }
-    if (inv_mass_b > 1e-8f) { set_xyz(&s.vel[ib], vb); set_xyz(&s.angvel[ib], wb); }
-    cr->impulses[0] = j_n;
-}
-
-__device__ void solve_contact(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr) {
-    if (cr->position_pen[3] < 0) return;
-    const uint32_t ia = cr->indices[0], ib = cr->indices[1];
-    contact_core(a, md, s, cr, s.pos[ia], s.pos[ib], s.vel[ia], s.vel[ib], s.angvel[ia], s.angvel[ib], cr->impulses[0]);
+    if (inv_mass > 1e-8f) {
+        set_xyz(&s.vel[me], v);
+        set_xyz(&s.angvel[me], w);
+    }
+    if (!odd) cr->impulses[0] = j_n;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -567,9 +562,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             const bool from_det = step == 0 && detached;
             for (uint32_t k = sl; k < pn; k += G) {
                 const ContactRec* r = from_det ? &a.prev_contacts[(size_t)env * M + k] : &s.con[s.perm[k]];
-                s.pkey[k] = pair_key(r->indices[0], r->indices[1]);
                 s.ppen[k] = *(const float4*)r->position_pen;
-                s.pimp[k] = *(const float4*)r->impulses;
+                s.pimp[k] = make_float4(r->impulses[0], r->impulses[1], r->impulses[2],
+                                        __uint_as_float(pair_key(r->indices[0], r->indices[1])));
             }
         }
         // ---- A: warm_start_constraints + apply_actions (:1408-1426, :196-229) ---------
@@ -753,12 +748,12 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 uint32_t lo = 0, hi = pn;
                 while (lo < hi) {
                     uint32_t mid = (lo + hi) >> 1;
-                    if (s.pkey[mid] < key) lo = mid + 1; else hi = mid;
+                    if (__float_as_uint(s.pimp[mid].w) < key) lo = mid + 1; else hi = mid;
                 }
                 const f3 p = mk3(c->position_pen[0], c->position_pen[1], c->position_pen[2]);
                 float best = 0.04f;
                 int best_i = -1;
-                for (uint32_t i = lo; i < pn && s.pkey[i] == key; ++i) {
+                for (uint32_t i = lo; i < pn && __float_as_uint(s.pimp[i].w) == key; ++i) {
                     const float4 q = s.ppen[i];
                     if (q.w < 0) continue;
                     f3 d = sub(mk3(q.x, q.y, q.z), p);
@@ -774,38 +769,61 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
         }
         // ---- Contact levels for S4 -----------------------------------------------------
-        // level(slot) = 1 + max level of earlier live slots sharing a body that the solve
+        // level(slot) = 1 + max level of earlier valid slots sharing a body that the solve
         // writes (inv_m > 1e-8). Running levels in order reproduces the sequential slot
-        // order exactly. The per-slot body pair is packed in parallel; one lane per env then
-        // scans the slots in order.
+        // order exactly. Valid slots (solve_contacts skips only pen < 0, :1667) are
+        // compacted in slot order with a ballot; one lane per env then assigns levels and
+        // counting-sorts the slots by level into s.lst, level l owning
+        // [s.loff[l - 1], s.loff[l]).
+        uint32_t nv = 0;
         if (live) {
-            for (uint32_t k = sl; k < n_live; k += G) {
-                const ContactRec* c = &s.con[s.perm[k]];
-                uint32_t info = 0xFFFFFFFFu;
-                if (!(c->position_pen[3] < 0)) {  // solve_contacts skips only pen < 0 (:1667)
-                    const uint32_t ia = c->indices[0], ib = c->indices[1];
-                    info = ((md.flags[ia] & 2u) ? ia : 0xFFFFu) | (((md.flags[ib] & 2u) ? ib : 0xFFFFu) << 16);
+            const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
+            const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
+            for (uint32_t base = 0; base < n_live; base += G) {
+                const uint32_t k = base + sl;
+                bool valid = false;
+                uint32_t phys = 0;
+                if (k < n_live) {
+                    phys = s.perm[k];
+                    valid = !(s.con[phys].position_pen[3] < 0);
                 }
-                s.skey[k] = info;
+                const uint64_t ballot = __ballot(valid);
+                if (valid) s.vlist[nv + (uint32_t)__popcll(ballot & below)] = (uint16_t)phys;
+                nv += (uint32_t)__popcll(ballot & group_mask);
             }
             for (uint32_t b = sl; b < B; b += G) s.last[b] = 0;
         }
         __syncthreads();
         if (live && sl == 0) {
             uint32_t nlev = 0;
-            for (uint32_t k = 0; k < n_live; ++k) {
-                const uint32_t info = s.skey[k];
-                uint32_t lv = 0;
-                if (info != 0xFFFFFFFFu) {
-                    const uint32_t ia = info & 0xFFFFu, ib = info >> 16;
-                    const uint32_t la = ia != 0xFFFFu ? s.last[ia] : 0u;
-                    const uint32_t lb = ib != 0xFFFFu ? s.last[ib] : 0u;
-                    lv = (la > lb ? la : lb) + 1;
-                    if (ia != 0xFFFFu) s.last[ia] = (uint16_t)lv;
-                    if (ib != 0xFFFFu) s.last[ib] = (uint16_t)lv;
-                    nlev = lv > nlev ? lv : nlev;
-                }
-                s.order[k] = (uint16_t)lv;
+            for (uint32_t i = 0; i < nv; ++i) {
+                const ContactRec* c = &s.con[s.vlist[i]];
+                const uint32_t ia = c->indices[0], ib = c->indices[1];
+                const bool da = (md.flags[ia] & 2u) != 0, db = (md.flags[ib] & 2u) != 0;
+                const uint32_t la = da ? s.last[ia] : 0u;
+                const uint32_t lb = db ? s.last[ib] : 0u;
+                const uint32_t lv = (la > lb ? la : lb) + 1;
+                if (da) s.last[ia] = (uint16_t)lv;
+                if (db) s.last[ib] = (uint16_t)lv;
+                s.order[i] = (uint16_t)lv;
+                nlev = lv > nlev ? lv : nlev;
+            }
+            // Counting sort: loff[l] = count, then the start of level l; placing the slots
+            // in slot order advances loff[l] to the end of level l, so level l ends up
+            // owning [loff[l - 1], loff[l]) with loff[0] = 0.
+            for (uint32_t l = 0; l <= nlev; ++l) s.loff[l] = 0;
+            for (uint32_t i = 0; i < nv; ++i) s.loff[s.order[i]] += 1;
+            uint32_t run = 0;
+            for (uint32_t l = 1; l <= nlev; ++l) {
+                const uint32_t c = s.loff[l];
+                s.loff[l] = (uint16_t)run;
+                run += c;
+            }
+            for (uint32_t i = 0; i < nv; ++i) {
+                const uint32_t lv = s.order[i];
+                const uint32_t at = s.loff[lv];
+                s.loff[lv] = (uint16_t)(at + 1);
+                s.lst[at] = s.vlist[i];
             }
             s.misc[2] = nlev;
         }
@@ -815,13 +833,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             const uint32_t* m2 = (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
             if (blockIdx.x * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
         }
-        // Each lane keeps the level of the slots it owns (sl, sl + G, ...) in registers.
-        uint16_t my_level[kMaxRecsPerLane];
-#pragma unroll
-        for (int r = 0; r < kMaxRecsPerLane; ++r) {
-            const uint32_t k = sl + r * G;
-            my_level[r] = (live && k < n_live) ? s.order[k] : (uint16_t)0;
-        }
+        const uint32_t my_nlev = live ? s.misc[2] : 0u;
         tick(PH_NARROW);
         // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
         // Phases are same-type runs inside a colour (build_joint_program); the type is
@@ -855,11 +867,14 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
         for (uint32_t it = 0; it < a.iters; ++it) {
             for (uint32_t lv = 1; lv <= max_lev; ++lv) {
-#pragma unroll
-                for (int r = 0; r < kMaxRecsPerLane; ++r) {
-                    if (my_level[r] == lv) solve_contact(a, md, s, &s.con[s.perm[sl + r * G]]);
+                if (live && lv <= my_nlev) {
+                    // Lane pair (2j, 2j+1) takes the j-th slot of the level.
+                    const bool odd = (sl & 1) != 0;
+                    const uint32_t end = s.loff[lv];
+                    for (uint32_t j = s.loff[lv - 1] + (sl >> 1); j < end; j += G / 2)
+                        solve_contact2(a, md, s, &s.con[s.lst[j]], odd);
                 }
-                __syncthreads();
+                wave_sync();
             }
         }
         tick(PH_CONTACTS);
