@@ -78,9 +78,9 @@ int zeno_amd_world_step_device(ZenoWorldHandle world, const float* d_actions, ui
 /* Waits for all work queued on the world's stream. */
 int zeno_amd_world_synchronize(ZenoWorldHandle world);
 
-/* Kernel timing with HIP events on the world's stream. enable != 0 starts recording an
- * event pair around every step launch; get returns the summed kernel time in ms and the
- * number of launches since the last reset (waits for the stream). */
+/* Kernel timing with HIP events on the world's stream. enable = k > 0 records an event pair
+ * around every k-th step launch (k = 1: every launch), 0 stops; get returns the summed
+ * kernel time in ms of the timed launches and their number (waits for the stream). */
 int zeno_amd_world_set_kernel_timing(ZenoWorldHandle world, int enable);
 int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, uint64_t* launches);
 

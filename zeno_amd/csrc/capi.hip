@@ -399,8 +399,9 @@ int zeno_amd_world_set_kernel_timing(ZenoWorldHandle world, int enable) {
     if (!world) return ZENO_INVALID_HANDLE;
     World* w = W(world);
     hipError_t e = w->sync();
-    w->timing = enable != 0;
+    w->timing = enable > 0 ? enable : 0;
     w->t_used = 0;
+    w->t_launch = 0;
     return hip_status(e, "set_kernel_timing");
 }
 

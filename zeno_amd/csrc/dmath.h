@@ -65,41 +65,37 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) { return fm
 
 // atan2 / asin after S. Moshier's Cephes single-precision routines (atanf.c, asinf.c):
 // reduction at tan(3pi/8) and tan(pi/8) with a degree-9 odd polynomial for atan; the 0.5
-// split with sqrt reduction and a degree-11 odd polynomial for asin. Max error 3 ulp.
+// split with sqrt reduction and a degree-11 odd polynomial for asin. Max error 3 ulp. The
+// CPU oracle evaluates the same operations (oracle/zeno_oracle.c).
 constexpr float kPi = 3.14159265358979323846f;
 constexpr float kPiO2 = 1.57079632679489661923f;
 constexpr float kPiO4 = 0.78539816339744830962f;
 
-__device__ __forceinline__ float atan_nonneg(float x) {
-    float y0, t;
-    if (x > 2.414213562373095f) { y0 = kPiO2; t = -1.0f / x; }
-    else if (x > 0.4142135623730950f) { y0 = kPiO4; t = (x - 1.0f) / (x + 1.0f); }
-    else { y0 = 0.0f; t = x; }
-    float z = t * t;
-    float p = (((8.05374449538e-2f * z - 1.38776856032e-1f) * z + 1.99777106478e-1f) * z - 3.33329491539e-1f) * z * t + t;
-    return y0 + p;
-}
-
+// atan2 without branches: every case of the branching form (NaN, x == 0, y == 0,
+// infinities, the three reduction ranges of atan) is evaluated and selected, so lanes do
+// not diverge. The reduction range selects the operands of its single division: -1 / q
+// above tan(3pi/8), (q - 1) / (q + 1) above tan(pi/8); each result equals the branching
+// form's bit for bit.
 __device__ __forceinline__ float z_atan2f(float y, float x) {
-    if (__builtin_isnan(x) || __builtin_isnan(y)) return x + y;
-    if (x == 0.0f) {
-        if (y > 0.0f) return kPiO2;
-        if (y < 0.0f) return -kPiO2;
-        return __builtin_signbit(x) ? (__builtin_signbit(y) ? -kPi : kPi) : y;
-    }
-    if (y == 0.0f) return __builtin_signbit(x) ? (__builtin_signbit(y) ? -kPi : kPi) : y;
-    float ax = __builtin_fabsf(x), ay = __builtin_fabsf(y);
-    float r;
-    if (__builtin_isinf(ax)) {
-        if (__builtin_isinf(ay)) r = x > 0.0f ? kPiO4 : 3.0f * kPiO4;
-        else r = x > 0.0f ? 0.0f : kPi;
-    } else if (__builtin_isinf(ay)) {
-        r = kPiO2;
-    } else {
-        float a = atan_nonneg(ay / ax);
-        r = x > 0.0f ? a : kPi - a;
-    }
-    return y < 0.0f ? -r : r;
+    const float ax = __builtin_fabsf(x), ay = __builtin_fabsf(y);
+    const float q = ay / ax;
+    const bool big = q > 2.414213562373095f, mid = q > 0.4142135623730950f;
+    const float num = big ? -1.0f : q - 1.0f;
+    const float den = big ? q : q + 1.0f;
+    const float t = mid ? num / den : q;
+    const float y0 = big ? kPiO2 : (mid ? kPiO4 : 0.0f);
+    const float z = t * t;
+    const float p = (((8.05374449538e-2f * z - 1.38776856032e-1f) * z + 1.99777106478e-1f) * z - 3.33329491539e-1f) * z * t + t;
+    const float at = y0 + p;
+    float r = x > 0.0f ? at : kPi - at;
+    const bool ix = __builtin_isinf(ax), iy = __builtin_isinf(ay);
+    r = ix ? (iy ? (x > 0.0f ? kPiO4 : 3.0f * kPiO4) : (x > 0.0f ? 0.0f : kPi)) : (iy ? kPiO2 : r);
+    float res = y < 0.0f ? -r : r;
+    const float on_axis = __builtin_signbit(x) ? (__builtin_signbit(y) ? -kPi : kPi) : y;  // y == 0 (and x == 0, y == 0)
+    const float x_zero = y > 0.0f ? kPiO2 : (y < 0.0f ? -kPiO2 : on_axis);
+    res = y == 0.0f ? on_axis : res;
+    res = x == 0.0f ? x_zero : res;
+    return (__builtin_isnan(x) || __builtin_isnan(y)) ? x + y : res;
 }
 
 __device__ __forceinline__ float z_asinf(float x) {

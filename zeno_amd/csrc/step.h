@@ -65,7 +65,8 @@ constexpr uint32_t kJRecQuads = 7;  // float4 per solve record
 struct JointPhase { uint32_t type, start, count, pad; };
 
 // Record layout (float4 quads):
-//   q0 = (ia, ib, template index, flags: bit0 inv_m_a > 0, bit1 inv_m_b > 0)  [u32]
+//   q0 = (ia, ib, template index, flags)  [u32]; flags: bit0 inv_m_a > 0, bit1 inv_m_b > 0,
+//        bit2 / bit3 the centre of mass of body a / b is exactly +0
 //   q1 = inverse mass and inertia of body a, q2 = of body b
 //   q3.w = compliance (replaced by compliance / dt^2 in LDS at kernel start)
 //   POSITIONAL: q3.xyz anchor_a, q4.xyz anchor_b, q5.xyz com_a, q6.xyz com_b
@@ -100,7 +101,14 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
                 if (ma[0] + mb[0] < 1e-8f) continue;  // all_shaders.metal:924: nothing to move
                 float4 q[kJRecQuads];
                 for (auto& x : q) x = make_float4(0, 0, 0, 0);
-                q[0] = make_float4(u(ia), u(ib), u(k), u((ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u)));
+                auto pos_zero = [](const float* v) {  // all three components +0.0f
+                    uint32_t b[3];
+                    std::memcpy(b, v, 12);
+                    return (b[0] | b[1] | b[2]) == 0u;
+                };
+                const uint32_t flags = (ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u) |
+                                       (pos_zero(com + 4 * ia) ? 4u : 0u) | (pos_zero(com + 4 * ib) ? 8u : 0u);
+                q[0] = make_float4(u(ia), u(ib), u(k), u(flags));
                 q[1] = make_float4(ma[0], ma[1], ma[2], ma[3]);
                 q[2] = make_float4(mb[0], mb[1], mb[2], mb[3]);
                 const float* A = t.anchor_a;

@@ -157,7 +157,12 @@ __device__ __forceinline__ void solve_positional2(const float4* r, const Lds& s,
         const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
         if (!odd) s.lam[ci] = lambda_prev + d_lambda;
         const f3 impulse = sscale(d_lambda, n);
-        const f3 rc = sub(rr, qrot(xyz(com), Q));
+        // r - qrot(com, q): with com = +0 and a finite q the rotated offset is exactly +0 and
+        // r - (+0) = r, so the rotation is skipped.
+        const bool com_zero = ((fbits(q0.w) >> (odd ? 3 : 2)) & 1u) != 0 && __builtin_isfinite(Q.x) &&
+                              __builtin_isfinite(Q.y) && __builtin_isfinite(Q.z) && __builtin_isfinite(Q.w);
+        f3 rc = rr;
+        if (!com_zero) rc = sub(rr, qrot(xyz(com), Q));
         if (inv_mass > 0) {
             set_xyz(&s.pos[me], add(P, signed3(sg, scale(impulse, inv_mass))));
             s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(cross(rc, impulse), iI), Q)))));

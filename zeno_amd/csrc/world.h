@@ -71,9 +71,10 @@ struct World {
     unsigned long long* d_phase = nullptr;  // [kPhaseCount] wall-clock ticks of workgroup 0
     double wall_clock_hz = 100e6;
     ZenoProfilingData prof{};
-    bool timing = false;
+    int timing = 0;                    // 0 off, k > 0: event pair around every k-th launch
+    uint64_t t_launch = 0;             // launches since timing was set
     std::vector<hipEvent_t> t_events;  // pairs
-    size_t t_used = 0;                 // events used (2 per launch)
+    size_t t_used = 0;                 // events used (2 per timed launch)
 
     ~World();
     static World* create(const Scene& scene, const ZenoConfig& cfg, std::string& err);

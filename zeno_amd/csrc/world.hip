@@ -298,7 +298,8 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.prev_detached_out = d_prev_detached;
     a.lds = lds;
     hipEvent_t t0 = nullptr, t1 = nullptr;
-    if (timing) {
+    const bool timed = timing > 0 && (t_launch++ % (uint64_t)timing) == 0;
+    if (timed) {
         while (t_events.size() < t_used + 2) {
             hipEvent_t ev;
             ZA_TRY(hipEventCreate(&ev));
@@ -315,7 +316,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     }
     ZA_TRY(launch_step(a, epw, stream));
     if (profiling) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
-    if (timing) ZA_TRY(hipEventRecord(t1, stream));
+    if (timed) ZA_TRY(hipEventRecord(t1, stream));
     mark_all_dirty();
     return hipSuccess;
 }

@@ -359,8 +359,9 @@ class ZenoWorld:
         if rc != 0:
             raise RuntimeError(f"synchronize failed: {rc}: {L.last_error()}")
 
-    def set_kernel_timing(self, enable: bool) -> None:
-        self._lib.zeno_amd_world_set_kernel_timing(self._handle, 1 if enable else 0)
+    def set_kernel_timing(self, enable, every: int = 1) -> None:
+        """Records HIP events around every `every`-th step launch (enable False stops)."""
+        self._lib.zeno_amd_world_set_kernel_timing(self._handle, int(every) if enable else 0)
 
     def get_kernel_timing(self) -> Tuple[float, int]:
         ms = C.c_double()
