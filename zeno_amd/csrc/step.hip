@@ -364,20 +364,21 @@ __device__ __forceinline__ void solve_slider(const float4* r, const Lds& s) {
 // solve_contacts on a lane pair: the even lane owns body a, the odd lane body b (see the
 // joint lane pairs). Operands keep the reference's order; body b's updates, which the
 // reference subtracts, are added with a factor of -1.
-__device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* cr,
+__device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t phys,
                                                bool odd) {
+    ContactRec* cr = &s.con[phys];
     const float4 pp = *(const float4*)cr->position_pen;
     const float4 nf = *(const float4*)cr->normal_friction;
+    const float4 aux = s.pimp[phys];  // (bias, correction share a, share b, inverse mass sum)
     const uint32_t ia = cr->indices[0], ib = cr->indices[1];
     const uint32_t me = odd ? ib : ia;
     const float4 imi = md.invmi[me];
     const float inv_mass = imi.x;
     const f3 iI = mk3(imi.y, imi.z, imi.w);
-    const float inv_mass_o = pair_swap(inv_mass);
-    const float inv_mass_sum = odd ? inv_mass_o + inv_mass : inv_mass + inv_mass_o;
+    const float inv_mass_sum = aux.w;
     if (inv_mass_sum < 1e-8f) return;
     const f3 normal = mk3(nf.x, nf.y, nf.z);
-    const float penetration = pp.w, friction = nf.w;
+    const float friction = nf.w;
     const f3 cp = mk3(pp.x, pp.y, pp.z);
     const float4 P0 = s.pos[me], V0 = s.vel[me], W0 = s.angvel[me];
     const float sg = odd ? -1.0f : 1.0f;
@@ -392,19 +393,17 @@ __device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md,
     const float tn = inv_mass + dot(mul(rn, iI), rn);
     const float w_normal = tn + pair_swap(tn);
     if (w_normal < 1e-8f) return;
-    const float bias = a.baumgarte * fmaxf(penetration - a.slop, 0.0f) / a.dt;
+    const float bias = aux.x;
     const float restitution = cr->impulses[3];
     const float vel_restitution = vel_normal < -0.5f ? restitution * vel_normal : 0.0f;
     float j_n = (-(vel_normal + vel_restitution) + bias) / w_normal;
     j_n = fmaxf(j_n, 0.0f);
     const f3 impulse_n = sscale(j_n, normal);
-    const float pos_correction = a.baumgarte * fmaxf(penetration - a.slop, 0.0f);
     f3 v = xyz(V0), w = xyz(W0);
     if (inv_mass > 1e-8f) {
         v = add(v, signed3(sg, scale(impulse_n, inv_mass)));
         w = add(w, signed3(sg, mul(cross(r, impulse_n), iI)));
-        const float ratio = inv_mass / inv_mass_sum;
-        set_xyz(&s.pos[me], add(xyz(P0), signed3(sg, sscale(pos_correction * ratio, normal))));
+        set_xyz(&s.pos[me], add(xyz(P0), signed3(sg, sscale(odd ? aux.z : aux.y, normal))));
     }
     const float j_n_acc = cr->impulses[0] + j_n;
     if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
@@ -832,6 +831,21 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
             s.misc[2] = nlev;
         }
+        // Per-slot constants of the contact solve (the same in every iteration): the bias
+        // velocity, the two position-correction shares and the summed inverse mass, kept in
+        // the snapshot's impulse array, which is dead once matching is done.
+        if (live) {
+            for (uint32_t i = sl; i < nv; i += G) {
+                const uint32_t phys = s.vlist[i];
+                const ContactRec* c = &s.con[phys];
+                const float inv_mass_a = md.invmi[c->indices[0]].x, inv_mass_b = md.invmi[c->indices[1]].x;
+                const float inv_mass_sum = inv_mass_a + inv_mass_b;
+                const float pos_correction = a.baumgarte * fmaxf(c->position_pen[3] - a.slop, 0.0f);
+                const float bias = pos_correction / a.dt;
+                s.pimp[phys] = make_float4(bias, pos_correction * (inv_mass_a / inv_mass_sum),
+                                           pos_correction * (inv_mass_b / inv_mass_sum), inv_mass_sum);
+            }
+        }
         __syncthreads();
         uint32_t max_lev = 0;
         for (int e2 = 0; e2 < EPW; ++e2) {
@@ -877,7 +891,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     const bool odd = (sl & 1) != 0;
                     const uint32_t end = s.loff[lv];
                     for (uint32_t j = s.loff[lv - 1] + (sl >> 1); j < end; j += G / 2)
-                        solve_contact2(a, md, s, &s.con[s.lst[j]], odd);
+                        solve_contact2(a, md, s, s.lst[j], odd);
                 }
                 wave_sync();
             }
