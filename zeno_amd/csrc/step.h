@@ -17,7 +17,7 @@ struct EnvLds {
     uint32_t lam;                                                      // float[N]
     uint32_t con;                                                      // ContactRec[M] (physical)
     uint32_t perm;                                                     // u16[M] logical -> physical
-    uint32_t skey;                                                     // u32[M] sort keys
+    uint32_t skey;                                                     // u32[M] sort keys (float4[J'] in stage C)
     uint32_t ppen, pimp;                                               // prev snapshot: float4[M] x2
     uint32_t order;                                                    // u16[M] level of each valid slot
     // Contact schedule, aliased onto arrays that are dead by then: vlist and lst (u16[M]
@@ -42,7 +42,7 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M) {
     L.lam = take(4 * (N > 0 ? N : 1));
     L.con = take(64 * M);
     L.perm = take(2 * M);
-    L.skey = take(4 * M);
+    L.skey = take(4 * M > 16 * Jp ? 4 * M : 16 * Jp);  // also the stage-C joint contributions
     L.ppen = take(16 * M); L.pimp = take(16 * M);
     L.order = take(2 * M);
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
@@ -148,6 +148,26 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
     }
 }
 
+// Joints acting on each body for apply_joint_forces (all_shaders.metal:122-190), in
+// ascending joint order: entry = joint index | bit 30 (body is the joint's parent, the
+// contribution is negated) | bit 31 (prismatic: force, else torque). Body 0 gets none.
+inline void build_body_joint_lists(const std::vector<JointRec>& joints, uint32_t B, std::vector<uint32_t>& off,
+                                   std::vector<uint32_t>& ent) {
+    off.assign(B + 1, 0);
+    ent.clear();
+    for (uint32_t b = 0; b < B; ++b) {
+        off[b] = (uint32_t)ent.size();
+        if (b == 0) continue;
+        for (uint32_t j = 0; j < joints.size(); ++j) {
+            const uint32_t ja = (uint32_t)joints[j].params[1], jb = (uint32_t)joints[j].params[2];
+            if (ja != b && jb != b) continue;
+            const bool prism = (uint32_t)joints[j].params[0] == JOINT_PRISMATIC;
+            ent.push_back(j | (ja == b ? (1u << 30) : 0u) | (prism ? (1u << 31) : 0u));
+        }
+    }
+    off[B] = (uint32_t)ent.size();
+}
+
 // Byte offsets of the per-scene model records inside the model blob. The blob is uploaded
 // once per world and copied into the front of every workgroup's LDS at kernel start, so
 // the solver phases never wait on global memory for model data.
@@ -160,6 +180,7 @@ struct ModelLayout {
     uint32_t sensors;            // SensorRec[S]
     uint32_t jrec;               // float4[kJRecQuads * R] joint solve records
     uint32_t jphase;             // JointPhase[nph]
+    uint32_t bjoff, bjl;         // u32[B + 1] offsets into u32[2J]: joints acting on each body
     uint32_t bytes;              // total, multiple of 16
 };
 
@@ -172,6 +193,7 @@ inline ModelLayout make_model_layout(uint32_t B, uint32_t J, uint32_t G, uint32_
     L.joints = take(80 * J); L.geoms = take(64 * G); L.pairs = take(4 * P);
     L.acts = take(32 * A); L.sensors = take(32 * S);
     L.jrec = take(16 * kJRecQuads * nrec); L.jphase = take(16 * nph);
+    L.bjoff = take(4 * (B + 1)); L.bjl = take(4 * 2 * J);
     L.bytes = o;
     return L;
 }

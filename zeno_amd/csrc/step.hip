@@ -39,6 +39,7 @@ struct Lds {
     uint16_t* perm;
     uint32_t* skey;
     float4 *ppen, *pimp;  // prev snapshot: position_pen; impulses.xyz with the pair key in .w
+    float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
     uint16_t *order, *vlist, *lst, *loff, *last;
     uint32_t* misc;
 };
@@ -55,6 +56,7 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.con = (ContactRec*)(base + L.con);
     s.perm = (uint16_t*)(base + L.perm);
     s.skey = (uint32_t*)(base + L.skey);
+    s.jw = (float4*)(base + L.skey);
     s.ppen = (float4*)(base + L.ppen); s.pimp = (float4*)(base + L.pimp);
     s.order = (uint16_t*)(base + L.order);
     s.vlist = (uint16_t*)(base + L.vlist);
@@ -77,6 +79,7 @@ struct Mdl {
     const SensorRec* sensors;
     const float4* jrec;
     const JointPhase* jph;
+    const uint32_t *bjoff, *bjl;
 };
 
 __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const ModelLayout& L) {
@@ -91,6 +94,8 @@ __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const Model
     m.sensors = (const SensorRec*)(base + L.sensors);
     m.jrec = (const float4*)(base + L.jrec);
     m.jph = (const JointPhase*)(base + L.jphase);
+    m.bjoff = (const uint32_t*)(base + L.bjoff);
+    m.bjl = (const uint32_t*)(base + L.bjl);
     return m;
 }
 
@@ -607,26 +612,41 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         __syncthreads();
         // ---- C: apply_joint_forces (S2) + save_prev_state (:122-190, :1900-1913) ------
+        // Each joint's world-frame contribution axis_world * tau is formed by one lane into
+        // jw (skipped when |tau| < 1e-6, flag w = 0); then each body sums the contributions
+        // of its joints in ascending joint order (build_body_joint_lists).
         if (live) {
-            for (uint32_t b = sl; b < B; b += G) {
-                if (b > 0) {
-                    float4 f = s.frc[b], t = s.trq[b];
-                    for (uint32_t j = 0; j < a.J; ++j) {
-                        const JointRec& jr = md.joints[j];
-                        const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
-                        if (ja != b && jb != b) continue;
-                        const float tau = s.jt[j];
-                        if (__builtin_fabsf(tau) < 1e-6f) continue;
-                        f3 w = scale(qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), toq(s.quat[ja])), tau);
-                        f3 d = ja == b ? neg(w) : w;
-                        if ((uint32_t)jr.params[0] == JOINT_PRISMATIC) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
-                        else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
-                    }
-                    s.frc[b] = f;
-                    s.trq[b] = t;
+            for (uint32_t j = sl; j < a.J; j += G) {
+                const JointRec& jr = md.joints[j];
+                const float tau = s.jt[j];
+                float4 c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (!(__builtin_fabsf(tau) < 1e-6f)) {
+                    const uint32_t ja = (uint32_t)jr.params[1];
+                    c = tof4(scale(qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), toq(s.quat[ja])), tau), 1.0f);
                 }
+                s.jw[j] = c;
+            }
+            for (uint32_t b = sl; b < B; b += G) {
                 s.ppos[b] = s.pos[b];
                 s.pquat[b] = s.quat[b];
+            }
+        }
+        __syncthreads();
+        if (live) {
+            for (uint32_t b = sl; b < B; b += G) {
+                const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
+                if (e0 == e1) continue;
+                float4 f = s.frc[b], t = s.trq[b];
+                for (uint32_t e = e0; e < e1; ++e) {
+                    const uint32_t ent = md.bjl[e];
+                    const float4 c = s.jw[ent & 0x3FFFFFFFu];
+                    if (c.w == 0.0f) continue;
+                    const f3 d = (ent & (1u << 30)) ? neg(xyz(c)) : xyz(c);
+                    if (ent & (1u << 31)) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
+                    else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
+                }
+                s.frc[b] = f;
+                s.trq[b] = t;
             }
         }
         __syncthreads();

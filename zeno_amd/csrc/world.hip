@@ -200,6 +200,10 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         put(w->ml.sensors, m.sensors.data(), sizeof(SensorRec) * m.sensors.size());
         put(w->ml.jrec, jrec.data(), sizeof(float4) * jrec.size());
         put(w->ml.jphase, jph.data(), sizeof(JointPhase) * jph.size());
+        std::vector<uint32_t> bjoff, bjl;
+        build_body_joint_lists(m.joints, w->B, bjoff, bjl);
+        put(w->ml.bjoff, bjoff.data(), 4 * bjoff.size());
+        put(w->ml.bjl, bjl.data(), 4 * bjl.size());
         if ((e = upload(w, &w->d_model, (const uint4*)blob.data(), w->ml.bytes / 16)) != hipSuccess) return fail("upload", e);
     }
     std::vector<float4> ip(w->B), iq(w->B), iv(w->B), ia(w->B);
