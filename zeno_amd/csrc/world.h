@@ -57,10 +57,15 @@ struct World {
     float* h_rewards = nullptr;
     uint8_t* h_dones = nullptr;
 
-    // Pinned action staging ring.
+    // Host actions: a pinned staging ring and a device ring, copied on their own stream so
+    // the copy for the next step overlaps the current step's kernel. act_copied[i] marks
+    // the copy into slot i done (the step waits on it), act_evt[i] the step that read it.
     static constexpr int kStage = 3;
+    hipStream_t cstream = nullptr;
     float* h_act[kStage] = {};
+    float* d_act_ring = nullptr;  // [kStage][E * A']
     hipEvent_t act_evt[kStage] = {};
+    hipEvent_t act_copied[kStage] = {};
     bool act_evt_used[kStage] = {};
     int act_slot = 0;
     uint8_t* h_mask_stage = nullptr;
@@ -93,6 +98,8 @@ struct World {
 
    private:
     hipError_t launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask);
+    hipError_t stage_actions(const float* actions, const float** d_out, int* slot);
+    hipError_t mark_actions_used(int slot);
     hipError_t upload_mask(const uint8_t* mask, uint8_t** d_out);
     hipError_t ensure_subset_buffers();
     void mark_all_dirty();

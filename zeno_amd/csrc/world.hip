@@ -97,6 +97,7 @@ World::~World() {
     for (int i = 0; i < kStage; ++i) {
         if (h_act[i]) hipHostFree(h_act[i]);
         if (act_evt[i]) hipEventDestroy(act_evt[i]);
+        if (act_copied[i]) hipEventDestroy(act_copied[i]);
     }
     if (h_mask_stage) hipHostFree(h_mask_stage);
     std::free(h_rewards);
@@ -104,6 +105,8 @@ World::~World() {
     if (prof_start) hipEventDestroy(prof_start);
     if (prof_stop) hipEventDestroy(prof_stop);
     for (hipEvent_t ev : t_events) hipEventDestroy(ev);
+    if (d_act_ring) hipFree(d_act_ring);
+    if (cstream) hipStreamDestroy(cstream);
     if (stream) hipStreamDestroy(stream);
 }
 
@@ -184,6 +187,8 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->epw = epw;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
+    if ((e = hipStreamCreateWithFlags(&w->cstream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
+    if ((e = dalloc(w, &w->d_act_ring, (size_t)kStage * w->E * w->Ap)) != hipSuccess) return fail("hipMalloc", e);
 
     // Model blob: every per-scene record the kernel reads, packed per ModelLayout.
     w->ml = ML;
@@ -264,6 +269,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     for (int i = 0; i < kStage; ++i) {
         if ((e = hipHostMalloc((void**)&w->h_act[i], (size_t)w->E * w->Ap * 4, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
         if ((e = hipEventCreateWithFlags(&w->act_evt[i], hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
+        if ((e = hipEventCreateWithFlags(&w->act_copied[i], hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
     }
     if ((e = hipHostMalloc((void**)&w->h_mask_stage, w->E, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
     if ((e = hipStreamSynchronize(w->stream)) != hipSuccess) return fail("init", e);
@@ -327,23 +333,40 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
 
 // World.step, world.zig:694-746: substeps 0 selects the configured count; dt = timestep /
 // substeps; accelerations come from the velocity change over the whole call.
+hipError_t World::stage_actions(const float* actions, const float** d_out, int* slot_out) {
+    const int slot = act_slot;
+    act_slot = (act_slot + 1) % kStage;
+    // The step that last read this slot (and the copy that fed it) must be done before the
+    // pinned and device buffers are reused.
+    if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
+    const size_t bytes = (size_t)E * A * sizeof(float);
+    float* d = d_act_ring + (size_t)slot * E * Ap;
+    std::memcpy(h_act[slot], actions, bytes);
+    ZA_TRY(hipMemcpyAsync(d, h_act[slot], bytes, hipMemcpyHostToDevice, cstream));
+    ZA_TRY(hipEventRecord(act_copied[slot], cstream));
+    ZA_TRY(hipStreamWaitEvent(stream, act_copied[slot], 0));
+    *d_out = d;
+    *slot_out = slot;
+    return hipSuccess;
+}
+
+hipError_t World::mark_actions_used(int slot) {
+    ZA_TRY(hipEventRecord(act_evt[slot], stream));
+    act_evt_used[slot] = true;
+    return hipSuccess;
+}
+
 hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_device) {
     ZA_TRY(hipSetDevice(device));
     const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
     dt = timestep / (float)std::max<uint32_t>(actual, 1);
     const float* d_act = d_actions;
-    if (actions_on_device) {
-        d_act = actions;
-    } else if (A > 0) {
-        const int slot = act_slot;
-        act_slot = (act_slot + 1) % kStage;
-        if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
-        std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
-        ZA_TRY(hipMemcpyAsync(d_actions, h_act[slot], (size_t)E * A * sizeof(float), hipMemcpyHostToDevice, stream));
-        ZA_TRY(hipEventRecord(act_evt[slot], stream));
-        act_evt_used[slot] = true;
-    }
-    return launch(d_act, actual, nullptr);
+    int slot = -1;
+    if (actions_on_device) d_act = actions;
+    else if (A > 0) ZA_TRY(stage_actions(actions, &d_act, &slot));
+    ZA_TRY(launch(d_act, actual, nullptr));
+    if (slot >= 0) ZA_TRY(mark_actions_used(slot));
+    return hipSuccess;
 }
 
 hipError_t World::ensure_subset_buffers() {
@@ -377,18 +400,14 @@ hipError_t World::step_subset(const float* actions, const uint8_t* mask, uint32_
     ZA_TRY(ensure_subset_buffers());
     const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
     dt = timestep / (float)std::max<uint32_t>(actual, 1);
-    if (A > 0) {
-        const int slot = act_slot;
-        act_slot = (act_slot + 1) % kStage;
-        if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
-        std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
-        ZA_TRY(hipMemcpyAsync(d_actions, h_act[slot], (size_t)E * A * sizeof(float), hipMemcpyHostToDevice, stream));
-        ZA_TRY(hipEventRecord(act_evt[slot], stream));
-        act_evt_used[slot] = true;
-    }
+    const float* d_act = d_actions;
+    int slot = -1;
+    if (A > 0) ZA_TRY(stage_actions(actions, &d_act, &slot));
     uint8_t* dm = nullptr;
     ZA_TRY(upload_mask(mask, &dm));
-    return launch(d_actions, actual, dm);
+    ZA_TRY(launch(d_act, actual, dm));
+    if (slot >= 0) ZA_TRY(mark_actions_used(slot));
+    return hipSuccess;
 }
 
 // World.reset, world.zig:1296-1314: restore the selected envs, then zero every env's
