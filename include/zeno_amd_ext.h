@@ -85,8 +85,20 @@ int zeno_amd_world_set_kernel_timing(ZenoWorldHandle world, int enable);
 int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, uint64_t* launches);
 
 /* Launch configuration chosen for the world: environments per wavefront and LDS bytes
- * per workgroup. */
+ * per workgroup (0 when the working sets live in HBM). */
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
+
+/* *hbm = 1 when the environments' working sets live in HBM (a scene whose model records
+ * plus one working set exceed a workgroup's LDS, or ZENO_AMD_WORKING_SET=hbm at create);
+ * *spatial_hash = 1 when the scene has more than 512 geoms and the spatial-hash broad
+ * phase runs (world.zig:534, all_shaders.metal:541-703). Either pointer may be null. */
+int zeno_amd_world_modes(ZenoWorldHandle world, int* hbm, int* spatial_hash);
+
+/* The spatial hash's cell of every geom in the last substep, [E*G] u32: x + 64 y + 4096 z
+ * of the clamped unit-cell coordinates, the reference's cell_ids buffer
+ * (world.zig:140,548; all_shaders.metal:576-582), which it keeps without a getter.
+ * ZENO_INVALID_ARGUMENT when the scene does not use the spatial hash. */
+int zeno_amd_world_get_cell_ids(ZenoWorldHandle world, uint32_t* out /* [E*G] */);
 
 #ifdef __cplusplus
 }

@@ -39,7 +39,7 @@ class ZoState(C.Structure):
         "positions", "quaternions", "velocities", "angular_velocities", "accelerations", "inv_mass_inertia",
         "forces", "torques", "prev_positions", "prev_quaternions", "prev_velocities",
         "joint_positions", "joint_velocities", "joint_torques", "observations",
-        "contacts", "contact_counts", "prev_contacts", "prev_contact_counts", "constraints")]
+        "contacts", "contact_counts", "prev_contacts", "prev_contact_counts", "constraints", "cell_ids")]
 
 
 _lib = None
@@ -65,6 +65,8 @@ def load() -> C.CDLL:
         lib.zo_match_cached.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]
         lib.zo_sort_contacts.restype = None
         lib.zo_sort_contacts.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32]
+        lib.zo_broad_phase_hash.restype = None
+        lib.zo_broad_phase_hash.argtypes = [C.POINTER(ZoModel), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         lib.zo_collide_env.restype = None
         lib.zo_collide_env.argtypes = [C.POINTER(ZoModel), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         _lib = lib
@@ -122,6 +124,7 @@ class OracleWorld:
         self.contact_counts = np.zeros(E, np.uint32)
         self.prev_contacts = np.zeros((E, M), CONTACT_DTYPE)
         self.prev_contact_counts = np.zeros(E, np.uint32)
+        self.cell_ids = np.zeros((E, max(model["num_geoms"], 1)), np.uint32)
         tmpl = model["constraints"]
         self.constraints = np.ascontiguousarray(np.broadcast_to(tmpl, (E, N)), CONSTRAINT_DTYPE).copy()
         if N:
@@ -244,6 +247,20 @@ def collide_env(world: "OracleWorld", env: int = 0) -> None:
                           _p(np.ascontiguousarray(world.quaternions[env])), _p(con), _p(cnt))
     world.contacts[env] = con
     world.contact_counts[env] = cnt[0]
+
+
+def broad_phase_hash(world: "OracleWorld", env: int = 0, count: int = 0):
+    """The spatial-hash broad phase alone on one env's current positions, at any geom count.
+
+    Returns (cell_ids [G] u32, contacts [M] with indices of the first min(n, M) pairs, n).
+    """
+    zm = world._model_struct()
+    G = world.model["num_geoms"]
+    ids = np.zeros(max(G, 1), np.uint32)
+    cnt = np.array([count], np.uint32)
+    con = np.zeros(world.M, CONTACT_DTYPE)
+    load().zo_broad_phase_hash(C.byref(zm), _p(np.ascontiguousarray(world.positions[env])), _p(ids), _p(con), _p(cnt))
+    return ids[:G], con, int(cnt[0])
 
 
 def atan2f(y: float, x: float) -> float:

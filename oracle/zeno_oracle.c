@@ -141,6 +141,7 @@ typedef struct {
     ZoContact *con, *pcon;
     uint32_t *count, *pcount;
     ZoConstraint* cs;
+    uint32_t* cell_ids; /* [G], spatial-hash mode */
 } Env;
 
 #define P4(arr, b) (&(arr)[4 * (size_t)(b)])
@@ -284,6 +285,102 @@ static void k_broad_phase(const ZoModel* m, const float* pos, uint32_t B_unused,
             }
         }
     }
+}
+
+/* ------------------------------------------------------------------------------------
+ * Spatial-hash broad phase (all_shaders.metal:556-703), which World.stepOnce runs instead
+ * of broad_phase when the scene has more than 512 geoms (world.zig:534,1043-1096): a
+ * 64^3 grid of unit cells (world.zig:542-563, inv_cell_size 1.0).
+ *
+ * Cell of a geom (:574-580): floor(pos * inv_cell_size) per axis, converted to int and
+ * clamped to [0, 63]. The GPU's float->int conversion saturates and maps NaN to 0, so a
+ * NaN, negative or huge coordinate lands in cell 0 or 63 of that axis.
+ *
+ * Emission order. The reference appends through an atomic counter from every thread at
+ * once, and its scatter/query barrier (:631) spans one threadgroup only, so its order is
+ * a race. This restatement runs it sequentially: every geom scattered (in ascending geom
+ * order, so each cell lists its geoms in ascending order) before any query; then geom g
+ * in ascending order queries dz, dy, dx = -1..1 (that loop nesting, :644-646) and the
+ * cell's geoms in list order, appending (body_a, body_b, g, other) for other > g that
+ * pass the same filters as broad_phase (:659-681). The set of pairs is the reference's;
+ * the order is one of its possible interleavings.
+ * ---------------------------------------------------------------------------------- */
+#define ZO_HASH_DIM 64u
+#define ZO_HASH_MIN_GEOMS 512u /* world.zig:534: hash when num_geoms > 512 */
+
+static uint32_t hash_axis(float p) {
+    float f = floorf(p * 1.0f);
+    if (!(f >= 0.0f)) return 0u; /* negative, or NaN (converts to 0) */
+    if (f >= (float)(ZO_HASH_DIM - 1u)) return ZO_HASH_DIM - 1u;
+    return (uint32_t)f;
+}
+
+static int cmp_u64(const void* a, const void* b) {
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+static void k_broad_phase_hash(const ZoModel* m, const float* pos, uint32_t* cell_ids, ZoContact* con, uint32_t* count) {
+    const uint32_t G = m->num_geoms, M = m->max_contacts, D = ZO_HASH_DIM;
+    uint32_t* cx = (uint32_t*)malloc(sizeof(uint32_t) * 3 * (G ? G : 1));
+    uint64_t* cells = (uint64_t*)malloc(sizeof(uint64_t) * (G ? G : 1)); /* (cell << 32) | geom */
+    /* broad_phase_count_cells (:556-584) */
+    for (uint32_t g = 0; g < G; ++g) {
+        const ZoGeom* ga = &m->geoms[g];
+        v3 p = vadd(ld3(P4(pos, ga->type_body[1])), ld3(ga->pos_size0));
+        cx[3 * g + 0] = hash_axis(p.x);
+        cx[3 * g + 1] = hash_axis(p.y);
+        cx[3 * g + 2] = hash_axis(p.z);
+        uint32_t id = cx[3 * g + 0] + cx[3 * g + 1] * D + cx[3 * g + 2] * D * D;
+        if (cell_ids) cell_ids[g] = id;
+        cells[g] = ((uint64_t)id << 32) | g;
+    }
+    /* broad_phase_prefix_sum + scatter (:588-629): the cells' lists back to back */
+    qsort(cells, G, sizeof(uint64_t), cmp_u64);
+    /* broad_phase_detect queries (:632-700) */
+    for (uint32_t g = 0; g < G; ++g) {
+        const ZoGeom* ga = &m->geoms[g];
+        uint32_t body_a = ga->type_body[1];
+        v3 pos_a = vadd(ld3(P4(pos, body_a)), ld3(ga->pos_size0));
+        float radius_a = ga->pos_size0[3];
+        uint32_t type_a = ga->type_body[0], group_a = ga->type_body[3], mask_a = ga->type_body[2];
+        for (int dz = -1; dz <= 1; ++dz) for (int dy = -1; dy <= 1; ++dy) for (int dx = -1; dx <= 1; ++dx) {
+            int nx = (int)cx[3 * g + 0] + dx, ny = (int)cx[3 * g + 1] + dy, nz = (int)cx[3 * g + 2] + dz;
+            if (nx < 0 || ny < 0 || nz < 0 || nx >= (int)D || ny >= (int)D || nz >= (int)D) continue;
+            uint64_t ncid = (uint64_t)((uint32_t)nx + (uint32_t)ny * D + (uint32_t)nz * D * D);
+            /* first list entry of cell ncid */
+            uint32_t lo = 0, hi = G;
+            while (lo < hi) {
+                uint32_t mid = lo + (hi - lo) / 2;
+                if ((cells[mid] >> 32) < ncid) lo = mid + 1; else hi = mid;
+            }
+            for (uint32_t s = lo; s < G && (cells[s] >> 32) == ncid; ++s) {
+                uint32_t o = (uint32_t)(cells[s] & 0xFFFFFFFFu);
+                if (o <= g) continue;
+                const ZoGeom* gb = &m->geoms[o];
+                uint32_t body_b = gb->type_body[1];
+                if (body_a == body_b) continue;
+                uint32_t group_b = gb->type_body[3], mask_b = gb->type_body[2];
+                if ((group_a & mask_b) == 0 && (group_b & mask_a) == 0) continue;
+                uint32_t type_b = gb->type_body[0];
+                v3 pos_b = vadd(ld3(P4(pos, body_b)), ld3(gb->pos_size0));
+                float radius_b = gb->pos_size0[3];
+                if (!(type_a == 3 || type_b == 3)) {
+                    v3 diff = vsub(pos_b, pos_a);
+                    float dist_sq = vdot(diff, diff);
+                    float min_dist = radius_a + radius_b + 0.1f;
+                    if (dist_sq >= min_dist * min_dist) continue;
+                }
+                uint32_t c = (*count)++;
+                if (c < M) {
+                    ZoContact* ct = &con[c];
+                    ct->indices[0] = body_a; ct->indices[1] = body_b; ct->indices[2] = g; ct->indices[3] = o;
+                }
+            }
+        }
+    }
+    free(cells);
+    free(cx);
 }
 
 /* sort_contacts, :711-745 (stable insertion sort by (min<<16)|max) */
@@ -843,7 +940,8 @@ static void step_once(Env* e, const float* actions) {
     k_apply_joint_forces(e);
     k_save_prev(e);
     k_integrate(e);
-    k_broad_phase(e->m, e->pos, e->B, e->con, e->count);
+    if (e->m->num_geoms > ZO_HASH_MIN_GEOMS) k_broad_phase_hash(e->m, e->pos, e->cell_ids, e->con, e->count);
+    else k_broad_phase(e->m, e->pos, e->B, e->con, e->count);
     k_sort_contacts(e->M, e->con, *e->count);
     k_narrow_phase(e->m, e->pos, e->con, *e->count);
     k_match_cached(e);
@@ -886,6 +984,7 @@ static void bind_env(const ZoModel* m, ZoState* s, uint32_t env, float dt, Env* 
     e->count = s->contact_counts + env;
     e->pcount = s->prev_contact_counts + env;
     e->cs = s->constraints + (size_t)e->N * env;
+    e->cell_ids = s->cell_ids ? s->cell_ids + (size_t)m->num_geoms * env : NULL;
 }
 
 int zo_step(const ZoModel* m, ZoState* s, const float* actions, uint32_t substeps,
@@ -931,6 +1030,11 @@ void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,
     k_match_cached(&e);
 }
 
+void zo_broad_phase_hash(const ZoModel* m, const float* positions, uint32_t* cell_ids,
+                         ZoContact* contacts, uint32_t* count) {
+    k_broad_phase_hash(m, positions, cell_ids, contacts, count);
+}
+
 void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count) {
     k_sort_contacts(max_contacts, contacts, count);
 }
@@ -938,7 +1042,13 @@ void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count
 void zo_collide_env(const ZoModel* m, const float* positions, const float* quaternions,
                     ZoContact* contacts, uint32_t* count) {
     (void)quaternions;
-    k_broad_phase(m, positions, m->num_bodies, contacts, count);
+    if (m->num_geoms > ZO_HASH_MIN_GEOMS) {
+        uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * m->num_geoms);
+        k_broad_phase_hash(m, positions, ids, contacts, count);
+        free(ids);
+    } else {
+        k_broad_phase(m, positions, m->num_bodies, contacts, count);
+    }
     k_sort_contacts(m->max_contacts, contacts, *count);
     k_narrow_phase(m, positions, contacts, *count);
 }

@@ -75,6 +75,7 @@ typedef struct {
     ZoContact* prev_contacts;   /* [E*M] */
     uint32_t* prev_contact_counts; /* [E] */
     ZoConstraint* constraints;  /* [E*N] */
+    uint32_t* cell_ids;         /* [E*G] spatial-hash cell of each geom (G > 512); may be NULL otherwise */
 } ZoState;
 
 /* World.step (world.zig:694-746) for envs [env_begin, env_end): copies actions, runs
@@ -100,6 +101,12 @@ float zo_asinf(float x);
  * 711-894), exposed for unit tests: positions are [B*4] of that env. */
 void zo_collide_env(const ZoModel* m, const float* positions, const float* quaternions,
                     ZoContact* contacts, uint32_t* count);
+
+/* The spatial-hash broad phase (all_shaders.metal:556-703) for one env, whatever the geom
+ * count, exposed for unit tests: cell_ids receives [G] cell ids; pairs are appended at
+ * *count in the sequential order described in zeno_oracle.c. */
+void zo_broad_phase_hash(const ZoModel* m, const float* positions, uint32_t* cell_ids,
+                         ZoContact* contacts, uint32_t* count);
 
 /* match_cached_contacts (all_shaders.metal:1483-1544) on one env, exposed for unit tests. */
 void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,

@@ -77,20 +77,26 @@ def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, ato
 
 
 def make_pair(name: str, num_envs: int, steps: int, seed: int = 0, envs_per_wave: Optional[int] = None,
-              substeps: int = 1, max_contacts: int = 64, contact_iterations: int = 4):
+              substeps: int = 1, max_contacts: int = 64, contact_iterations: int = 4,
+              working_set: Optional[str] = None):
+    """GPU world and oracle on the same seeded state. envs_per_wave / working_set ("hbm")
+    override the launch shape the world would choose."""
     path, xml, model, state, acts = workload_inputs(name, num_envs, steps, seed)
-    old = os.environ.get("ZENO_AMD_ENVS_PER_WAVE")
+    overrides = {"ZENO_AMD_ENVS_PER_WAVE": None if envs_per_wave is None else str(envs_per_wave),
+                 "ZENO_AMD_WORKING_SET": working_set}
+    saved = {k: os.environ.get(k) for k in overrides}
     try:
-        if envs_per_wave is not None:
-            os.environ["ZENO_AMD_ENVS_PER_WAVE"] = str(envs_per_wave)
+        for k, v in overrides.items():
+            if v is not None:
+                os.environ[k] = v
         g = ZenoWorld(mjcf_path=path, mjcf_string=xml, num_envs=num_envs, substeps=substeps,
                       max_contacts_per_env=max_contacts, contact_iterations=contact_iterations)
     finally:
-        if envs_per_wave is not None:
-            if old is None:
-                os.environ.pop("ZENO_AMD_ENVS_PER_WAVE", None)
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
             else:
-                os.environ["ZENO_AMD_ENVS_PER_WAVE"] = old
+                os.environ[k] = v
     o = OracleWorld(model, num_envs, max_contacts_per_env=max_contacts, substeps=substeps,
                     contact_iterations=contact_iterations)
     g.reset_to_state(*state)

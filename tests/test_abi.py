@@ -92,7 +92,8 @@ def test_null_handles(lib):
                   "memory_usage", "max_contacts_per_env"]:
         assert getattr(lib, f"zeno_world_{count}")(null) == 0, count
     for ext in ["world_get_lambda", "world_get_prev_contact_counts", "world_synchronize",
-                "world_set_kernel_timing", "world_model_view", "world_launch_config"]:
+                "world_set_kernel_timing", "world_model_view", "world_launch_config", "world_modes",
+                "world_get_cell_ids"]:
         fn = getattr(lib, f"zeno_amd_{ext}")
         args = [None] * len(fn.argtypes)
         if ext == "world_set_kernel_timing":

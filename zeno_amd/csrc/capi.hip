@@ -413,9 +413,27 @@ int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, ui
 
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes) {
     if (!world) return ZENO_INVALID_HANDLE;
-    if (envs_per_wave) *envs_per_wave = (uint32_t)W(world)->epw;
-    if (lds_bytes) *lds_bytes = W(world)->lds.bytes * (uint32_t)W(world)->epw;
+    const World* w = W(world);
+    if (envs_per_wave) *envs_per_wave = (uint32_t)w->epw;
+    if (lds_bytes) *lds_bytes = w->hbm ? 0u : w->ml.bytes + w->lds.bytes * (uint32_t)w->epw;
     return ZENO_SUCCESS;
+}
+
+int zeno_amd_world_modes(ZenoWorldHandle world, int* hbm, int* spatial_hash) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    if (hbm) *hbm = W(world)->hbm ? 1 : 0;
+    if (spatial_hash) *spatial_hash = W(world)->hash ? 1 : 0;
+    return ZENO_SUCCESS;
+}
+
+int zeno_amd_world_get_cell_ids(ZenoWorldHandle world, uint32_t* out) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    World* w = W(world);
+    if (!out || !w->hash) return ZENO_INVALID_ARGUMENT;
+    hipError_t e = hipSetDevice(w->device);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, w->d_cell_ids, (size_t)w->E * w->model.num_geoms * 4, hipMemcpyDeviceToHost, w->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
+    return hip_status(e, "get_cell_ids");
 }
 
 }  // extern "C"

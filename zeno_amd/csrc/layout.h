@@ -14,6 +14,11 @@
 
 namespace za {
 
+// Spatial hash (all_shaders.metal:541-703, world.zig:533-569): used above 512 geoms, over a
+// 64^3 grid of unit cells. The step kernel's sort key packs the geom index into 14 bits.
+constexpr uint32_t kHashMinGeoms = 512;
+constexpr uint32_t kHashMaxGeoms = 1u << 14;
+
 // BodyDataGPU, src/world/world.zig:1573-1597 (80 B):
 // position, quaternion (xyzw), inv_mass_inertia (inv_m, invI.xyz),
 // params (parent_id, body_type, gravity_scale, linear_damping), com_offset.

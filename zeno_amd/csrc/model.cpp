@@ -324,10 +324,12 @@ void build_model(const Scene& s, Model& m) {
 
     // Candidate geom pairs: the broad phase's static filters (same body, contype /
     // conaffinity, all_shaders.metal:494-506) depend only on the model, so they are
-    // applied once here. The list keeps (g, g') lexicographic order.
+    // applied once here. The list keeps (g, g') lexicographic order. Scenes above
+    // kHashMinGeoms geoms use the spatial hash instead (world.zig:534) and keep no list.
     m.pairs.clear();
-    for (uint32_t g = 0; g < m.num_geoms; ++g) {
-        for (uint32_t h = g + 1; h < m.num_geoms; ++h) {
+    const uint32_t listed = m.num_geoms > kHashMinGeoms ? 0u : m.num_geoms;
+    for (uint32_t g = 0; g < listed; ++g) {
+        for (uint32_t h = g + 1; h < listed; ++h) {
             const GeomRec& a = m.geoms[g];
             const GeomRec& b = m.geoms[h];
             if (a.type_body[1] == b.type_body[1]) continue;

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -10,7 +11,8 @@
 
 namespace za {
 
-// Byte offsets of one environment's working set in LDS. Every section is 16-byte aligned.
+// Byte offsets of one environment's working set (in LDS, or in HBM for scenes too large
+// for LDS). Every section is 16-byte aligned.
 struct EnvLds {
     uint32_t pos, quat, vel, angvel, ppos, pquat, frc, trq, vbefore;  // float4[B]
     uint32_t jt, jp, jv;                                               // float[J']
@@ -24,6 +26,12 @@ struct EnvLds {
     // each: valid slots, valid slots by level) share skey; loff (u16[M + 2], level ranges
     // in lst) shares ppen.
     uint32_t vlist, lst, loff;
+    // Spatial-hash broad phase (scenes above kHashMinGeoms geoms), on skey as well: hkey
+    // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom).
+    uint32_t hkey, hcell;
+    // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
+    // when the working set lives in HBM (the model blob is then read in place).
+    uint32_t jrec;
     uint32_t last;                                                     // u16[B]
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
     uint32_t bytes;                                                    // total, multiple of 16
@@ -31,10 +39,16 @@ struct EnvLds {
 
 inline uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
 
-inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M) {
+// Spatial-hash sort length: G rounded up to a power of two.
+inline uint32_t hash_pad(uint32_t G) { uint32_t p = 1; while (p < G) p <<= 1; return p; }
+
+// G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
+// solve records when they are copied per environment (HBM working set), else 0.
+inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint32_t G = 0, uint32_t jrec_bytes = 0) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
+    const uint32_t hash_bytes = G > kHashMinGeoms ? 4 * (hash_pad(G) + G) : 0;
     L.pos = take(16 * B); L.quat = take(16 * B); L.vel = take(16 * B); L.angvel = take(16 * B);
     L.ppos = take(16 * B); L.pquat = take(16 * B); L.frc = take(16 * B); L.trq = take(16 * B);
     L.vbefore = take(16 * B);
@@ -42,11 +56,13 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M) {
     L.lam = take(4 * (N > 0 ? N : 1));
     L.con = take(64 * M);
     L.perm = take(2 * M);
-    L.skey = take(4 * M > 16 * Jp ? 4 * M : 16 * Jp);  // also the stage-C joint contributions
+    L.skey = take(std::max(std::max(4 * M, 16 * Jp), hash_bytes));  // also stage-C joint contributions, hash
     L.ppen = take(16 * M); L.pimp = take(16 * M);
     L.order = take(2 * M);
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
+    L.hkey = L.skey; L.hcell = L.skey + 4 * (G > kHashMinGeoms ? hash_pad(G) : 0);
+    L.jrec = take(jrec_bytes);
     L.last = take(2 * B);
     L.misc = take(16);
     L.bytes = o;
@@ -199,8 +215,9 @@ inline ModelLayout make_model_layout(uint32_t B, uint32_t J, uint32_t G, uint32_
 }
 
 struct StepArgs {
-    // Sizes.
-    uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P;
+    // Sizes. G = geoms; Gp = G rounded up to a power of two (hash mode).
+    uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P, G, Gp;
+    uint32_t hash;  // 1: spatial-hash broad phase (G > kHashMinGeoms), 0: candidate pair list
     uint32_t iters, substeps;
     // Scalars (SimParams, world.zig:35-56).
     float dt, inv_step, gx, gy, gz, restitution, baumgarte, slop;
@@ -226,6 +243,10 @@ struct StepArgs {
     uint8_t* prev_detached_out;     // [E]
     // Optional per-phase wall-clock ticks of workgroup 0 (profiling); null when unused.
     unsigned long long* phase_ticks; // [kPhaseCount]
+    uint32_t* cell_ids;             // [E*G] hash mode: each geom's cell in the last substep
+    // Working sets in HBM (scenes whose working set exceeds LDS): lds.bytes per
+    // environment, one environment per workgroup. Null: working sets in LDS.
+    unsigned char* work;
     EnvLds lds;
 };
 
@@ -235,7 +256,8 @@ enum Phase { PH_LOAD, PH_FORCES, PH_BROAD, PH_NARROW, PH_JOINTS, PH_CONTACTS, PH
 // Largest dynamic LDS allocation one workgroup may request on `device`.
 size_t max_lds_per_workgroup(int device);
 
-// Launches ceil(E / envs_per_wave) single-wave workgroups. envs_per_wave in {1,2,4,8}.
+// Launches ceil(E / envs_per_wave) single-wave workgroups. envs_per_wave in {1,2,4,8};
+// 1 when a.work is set (working sets in HBM).
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream);
 
 // Largest M supported for a given envs_per_wave (the sort and the contact schedule keep

@@ -41,6 +41,8 @@ struct Lds {
     float4 *ppen, *pimp;  // prev snapshot: position_pen; impulses.xyz with the pair key in .w
     float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
     uint16_t *order, *vlist, *lst, *loff, *last;
+    uint32_t *hkey, *hcell;  // spatial hash, aliased on skey
+    float4* jrec;            // per-environment solve records (HBM working sets)
     uint32_t* misc;
 };
 
@@ -63,6 +65,9 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.lst = (uint16_t*)(base + L.lst);
     s.loff = (uint16_t*)(base + L.loff);
     s.last = (uint16_t*)(base + L.last);
+    s.hkey = (uint32_t*)(base + L.hkey);
+    s.hcell = (uint32_t*)(base + L.hcell);
+    s.jrec = (float4*)(base + L.jrec);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
 }
@@ -108,11 +113,19 @@ __device__ __forceinline__ void set_xyz(float4* p, f3 v) { p->x = v.x; p->y = v.
 __device__ __forceinline__ uint32_t fbits(float x) { return __float_as_uint(x); }
 
 // Single-wave workgroups: LDS operations of one wave complete in program order, so a
-// compiler-level ordering point is all that is needed between dependent phases.
+// compiler-level ordering point is all that is needed between dependent phases. A
+// working set in HBM takes workgroup-scope fences (stores complete before later loads).
+template <bool HBM>
 __device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (HBM) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    } else {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 }
 
 // Lane pairs. The positional, hinge and angular-limit solves run on two adjacent lanes:
@@ -498,18 +511,96 @@ __device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, Cont
     }
 }
 
-template <int EPW>
+// ---------------------------------------------------------------------------------------
+// Spatial-hash broad phase, all_shaders.metal:556-703 (scenes above 512 geoms,
+// world.zig:534). The reference's dense per-env grid (64^3 counters and offsets, a serial
+// 262,144-cell scan per env) becomes a sorted list: every geom's key cell << 14 | geom is
+// sorted in the env's working set, and a geom's 3x3x3 neighbourhood is nine rows of three
+// consecutive cell ids, each found by binary search. Appends follow the sequential order
+// of the reference's loops: geom ascending, then dz, dy, dx, then geoms of a cell in
+// ascending order (the reference's atomic appends make any interleaving possible).
+// ---------------------------------------------------------------------------------------
+// Cell coordinate (:574-575): floor, GPU float->int conversion (NaN -> 0), clamp to [0, 63].
+__device__ __forceinline__ uint32_t hash_axis(float p) {
+    const float f = __builtin_floorf(p * 1.0f);
+    return !(f >= 0.0f) ? 0u : (f >= 63.0f ? 63u : (uint32_t)f);
+}
+
+// First position in key[0, n) whose cell is >= cell.
+__device__ __forceinline__ uint32_t hash_lower_bound(const uint32_t* key, uint32_t lo, uint32_t n, uint32_t cell) {
+    uint32_t hi = n;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if ((key[mid] >> 14) < cell) lo = mid + 1; else hi = mid;
+    }
+    return lo;
+}
+
+// Pairs (g, other > g) of one geom (:632-700). Returns their number; with emit set, writes
+// pair k to logical slot `slot + k` while that is below M.
+__device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t g, bool emit, uint32_t slot) {
+    const GeomRec& ga = md.geoms[g];
+    const uint32_t body_a = ga.type_body[1], type_a = ga.type_body[0];
+    const uint32_t mask_a = ga.type_body[2], group_a = ga.type_body[3];
+    const f3 pa = add(xyz(s.pos[body_a]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
+    const float ra = ga.pos_size0[3];
+    const uint32_t id = s.hcell[g];
+    const int cx = (int)(id & 63u), cy = (int)((id >> 6) & 63u), cz = (int)(id >> 12);
+    const uint32_t xlo = cx > 0 ? (uint32_t)cx - 1u : 0u, xhi = cx < 63 ? (uint32_t)cx + 1u : 63u;
+    uint32_t hits = 0;
+    for (int dz = -1; dz <= 1; ++dz) {
+        const int nz = cz + dz;
+        if (nz < 0 || nz > 63) continue;
+        for (int dy = -1; dy <= 1; ++dy) {
+            const int ny = cy + dy;
+            if (ny < 0 || ny > 63) continue;
+            const uint32_t row = (uint32_t)ny * 64u + (uint32_t)nz * 4096u;
+            uint32_t k = hash_lower_bound(s.hkey, 0, a.G, row + xlo);
+            const uint32_t end = hash_lower_bound(s.hkey, k, a.G, row + xhi + 1u);
+            for (; k < end; ++k) {
+                const uint32_t o = s.hkey[k] & 0x3FFFu;
+                if (o <= g) continue;
+                const GeomRec& gb = md.geoms[o];
+                const uint32_t body_b = gb.type_body[1];
+                if (body_a == body_b) continue;
+                if ((group_a & gb.type_body[2]) == 0 && (gb.type_body[3] & mask_a) == 0) continue;
+                if (!(type_a == GEOM_PLANE || gb.type_body[0] == GEOM_PLANE)) {
+                    const f3 pb = add(xyz(s.pos[body_b]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
+                    const f3 diff = sub(pb, pa);
+                    const float min_dist = ra + gb.pos_size0[3] + 0.1f;
+                    if (dot(diff, diff) >= min_dist * min_dist) continue;
+                }
+                if (emit && slot + hits < a.M) {
+                    uint32_t* idx = s.con[s.perm[slot + hits]].indices;
+                    idx[0] = body_a; idx[1] = body_b; idx[2] = g; idx[3] = o;
+                }
+                ++hits;
+            }
+        }
+    }
+    return hits;
+}
+
+// HBM = false: the model records and EPW working sets live in LDS. HBM = true (EPW 1):
+// the working set lives in a.work and the model blob is read in place, for scenes whose
+// working set does not fit in LDS.
+// HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms, one environment
+// per workgroup) instead of the candidate pair list.
+template <int EPW, bool HBM, bool HASH>
 __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
+    static_assert(!HBM || EPW == 1, "HBM working sets run one environment per workgroup");
+    static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int le = tid / G;
     const int sl = tid % G;
     const uint32_t env = blockIdx.x * EPW + le;
     const bool live = env < a.E;
-    unsigned char* const env_base = smem + a.ml.bytes;
+    unsigned char* const env_base = HBM ? a.work + (size_t)blockIdx.x * a.lds.bytes : smem + a.ml.bytes;
     const Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
-    const Mdl md = bind_model(smem, a.ml);
+    Mdl md = bind_model(HBM ? (const unsigned char*)a.model : smem, a.ml);
+    if (HBM) md.jrec = s.jrec;
     const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
     const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
 
@@ -526,12 +617,17 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     };
 
     // ---- Model records (one blob per scene) -> LDS -------------------------------------
-    for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
+    if (!HBM) {
+        for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
+    } else {
+        const uint4* src = a.model + a.ml.jrec / 16u;
+        for (uint32_t i = tid; i < a.nrec * kJRecQuads; i += kWave) ((uint4*)s.jrec)[i] = src[i];
+    }
     __syncthreads();
     // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
     // this launch: computed once per record.
     for (uint32_t i = tid; i < a.nrec; i += kWave) {
-        float4* q3 = (float4*)(smem + a.ml.jrec) + i * kJRecQuads + 3;
+        float4* q3 = (float4*)md.jrec + i * kJRecQuads + 3;
         q3->w = q3->w / (a.dt * a.dt);
     }
 
@@ -672,9 +768,55 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         __syncthreads();
         tick(PH_FORCES);
-        // ---- E: broad_phase (S1), :468-533 -------------------------------------------
+        // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
         const uint32_t count_before = count;
-        {
+        if (HASH) {
+            // Cells (broad_phase_count_cells, :556-584) and sort keys; padding keys sort last.
+            if (live) {
+                for (uint32_t g = sl; g < a.Gp; g += G) {
+                    uint32_t key = 0xFFFFFFFFu;
+                    if (g < a.G) {
+                        const GeomRec& gr = md.geoms[g];
+                        const f3 p = add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2]));
+                        const uint32_t id = hash_axis(p.x) + hash_axis(p.y) * 64u + hash_axis(p.z) * 4096u;
+                        s.hcell[g] = id;
+                        a.cell_ids[(size_t)env * a.G + g] = id;
+                        key = (id << 14) | g;
+                    }
+                    s.hkey[g] = key;
+                }
+            }
+            __syncthreads();
+            // Bitonic sort of the Gp keys: one compare-exchange pair per lane and pass.
+            for (uint32_t k = 2; k <= a.Gp; k <<= 1) {
+                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                    if (live) {
+                        for (uint32_t t = sl; t < a.Gp / 2; t += G) {
+                            const uint32_t i = ((t & ~(j - 1u)) << 1) | (t & (j - 1u));
+                            const uint32_t l = i | j;
+                            const uint32_t x = s.hkey[i], y = s.hkey[l];
+                            if ((x > y) == ((i & k) == 0)) { s.hkey[i] = y; s.hkey[l] = x; }
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
+            // Queries (broad_phase_detect, :632-700): count each geom's pairs, place them
+            // with a prefix sum over the env's lanes, then write them.
+            for (uint32_t base = 0; base < a.G; base += G) {
+                const uint32_t g = base + sl;
+                const bool mine = live && g < a.G;
+                const uint32_t h = mine ? hash_pairs_of(a, md, s, g, false, 0) : 0u;
+                uint32_t inc = h;
+                for (uint32_t d = 1; d < (uint32_t)G; d <<= 1) {
+                    const uint32_t t = __shfl_up(inc, d, G);
+                    if ((uint32_t)sl >= d) inc += t;
+                }
+                const uint32_t total = __shfl(inc, G - 1, G);
+                if (mine && h > 0 && count + (inc - h) < M) hash_pairs_of(a, md, s, g, true, count + (inc - h));
+                count += total;
+            }
+        } else {
             const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
             const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
             for (uint32_t base = 0; base < a.P; base += G) {
@@ -899,7 +1041,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                         }
                     }
                 }
-                wave_sync();
+                wave_sync<HBM>();
             }
         }
         tick(PH_JOINTS);
@@ -913,7 +1055,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     for (uint32_t j = s.loff[lv - 1] + (sl >> 1); j < end; j += G / 2)
                         solve_contact2(a, md, s, s.lst[j], odd);
                 }
-                wave_sync();
+                wave_sync<HBM>();
             }
         }
         tick(PH_CONTACTS);
@@ -1032,12 +1174,18 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     }
 }
 
-template <int EPW>
+#define ZA_CHECK(x)                      \
+    do {                                 \
+        hipError_t _e = (x);             \
+        if (_e != hipSuccess) return _e; \
+    } while (0)
+
+template <int EPW, bool HASH>
 hipError_t allow_lds(size_t shmem) {
     // Workgroups above 64 KB of dynamic LDS must opt in per kernel (gfx950 has 160 KB / CU).
     static size_t granted = 64 * 1024;
     if (shmem <= granted) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, false, HASH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e == hipSuccess) granted = shmem;
     return e;
 }
@@ -1053,21 +1201,30 @@ size_t max_lds_per_workgroup(int device) {
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
     if (a.E == 0) return hipSuccess;
     const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
+    if ((a.work != nullptr || a.hash) && envs_per_wave != 1) return hipErrorInvalidValue;
+    if (a.work != nullptr) {
+        if (a.hash) hipLaunchKernelGGL((step_kernel<1, true, true>), dim3(blocks), dim3(kWave), 0, stream, a);
+        else hipLaunchKernelGGL((step_kernel<1, true, false>), dim3(blocks), dim3(kWave), 0, stream, a);
+        return hipGetLastError();
+    }
     const size_t shmem = (size_t)a.ml.bytes + (size_t)a.lds.bytes * (size_t)envs_per_wave;
-    hipError_t e = hipSuccess;
+    if (a.hash) {
+        ZA_CHECK((allow_lds<1, true>(shmem)));
+        hipLaunchKernelGGL((step_kernel<1, false, true>), dim3(blocks), dim3(kWave), shmem, stream, a);
+        return hipGetLastError();
+    }
     switch (envs_per_wave) {
-        case 1: e = allow_lds<1>(shmem); break;
-        case 2: e = allow_lds<2>(shmem); break;
-        case 4: e = allow_lds<4>(shmem); break;
-        case 8: e = allow_lds<8>(shmem); break;
+        case 1: ZA_CHECK((allow_lds<1, false>(shmem))); break;
+        case 2: ZA_CHECK((allow_lds<2, false>(shmem))); break;
+        case 4: ZA_CHECK((allow_lds<4, false>(shmem))); break;
+        case 8: ZA_CHECK((allow_lds<8, false>(shmem))); break;
         default: return hipErrorInvalidValue;
     }
-    if (e != hipSuccess) return e;
     switch (envs_per_wave) {
-        case 1: hipLaunchKernelGGL(step_kernel<1>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 2: hipLaunchKernelGGL(step_kernel<2>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 4: hipLaunchKernelGGL(step_kernel<4>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 8: hipLaunchKernelGGL(step_kernel<8>, dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 1: hipLaunchKernelGGL((step_kernel<1, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 2: hipLaunchKernelGGL((step_kernel<2, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 4: hipLaunchKernelGGL((step_kernel<4, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 8: hipLaunchKernelGGL((step_kernel<8, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -30,6 +30,8 @@ struct World {
     int device = 0;
     int epw = 1;
     EnvLds lds{};
+    bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
+    bool hbm = false;   // working sets in HBM (d_work) instead of LDS
     hipStream_t stream = nullptr;
     size_t device_bytes = 0;
 
@@ -44,6 +46,8 @@ struct World {
     float* d_actions = nullptr;
     ContactRec* d_con = nullptr;
     uint32_t *d_counts = nullptr, *d_pcounts = nullptr;
+    uint32_t* d_cell_ids = nullptr;       // [E*G] hash mode
+    unsigned char* d_work = nullptr;      // [E * lds.bytes] HBM working sets
     // step_subset support, allocated on first use.
     ContactRec* d_prev_con = nullptr;
     uint8_t* d_prev_detached = nullptr;

@@ -91,7 +91,7 @@ World::~World() {
     if (stream) hipStreamSynchronize(stream);
     void* dev[] = {d_model, d_phase, d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
                    d_jpos, d_jvel, d_jtrq, d_obs, d_lam, d_actions, d_con, d_counts, d_pcounts, d_prev_con,
-                   d_prev_detached, d_mask, d_stage};
+                   d_prev_detached, d_mask, d_stage, d_cell_ids, d_work};
     for (void* p : dev) if (p) hipFree(p);
     for (int i = 0; i < MIR_COUNT_ALL; ++i) if (h_mirror[i]) hipHostFree(h_mirror[i]);
     for (int i = 0; i < kStage; ++i) {
@@ -148,10 +148,9 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     hipError_t e = hipGetDevice(&w->device);
     if (e != hipSuccess) return fail("hipGetDevice", e);
 
-    // Launch shape: the largest environments-per-wave that keeps at least ~one wave per
-    // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS.
-    const EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1));
-    w->lds = L;
+    w->hash = m.num_geoms > kHashMinGeoms;
+    if (w->hash && m.num_geoms > kHashMaxGeoms) { err = "scene too large for the spatial hash (over 16384 geoms)"; delete w; return nullptr; }
+    EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms);
     std::vector<float4> invmi(w->B), com(w->B);
     std::vector<uint32_t> flags(w->B);
     for (uint32_t b = 0; b < w->B; ++b) {
@@ -166,24 +165,32 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->nrec = (uint32_t)(jrec.size() / kJRecQuads);
     w->njph = (uint32_t)jph.size();
     const ModelLayout ML = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->nrec, w->njph);
+    // Launch shape: the largest environments-per-wave that keeps at least ~one wave per
+    // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS. A scene
+    // whose model records plus one working set exceed the workgroup's LDS keeps its
+    // working sets in HBM instead (one environment per wave); ZENO_AMD_WORKING_SET=hbm
+    // selects that path for any scene.
+    const char* ws = std::getenv("ZENO_AMD_WORKING_SET");
+    w->hbm = (ws && std::strcmp(ws, "hbm") == 0) || (size_t)ML.bytes + (size_t)L.bytes > max_lds_per_workgroup(w->device);
     int epw = 1;
-    for (int cand : {8, 4, 2}) {
-        if (w->M > max_contacts_for(cand)) continue;
-        if ((size_t)ML.bytes + (size_t)L.bytes * cand > 64 * 1024) continue;
-        if ((w->E + cand - 1) / cand < 1024) continue;
-        epw = cand;
-        break;
-    }
-    if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) {
-        int v = std::atoi(env);
-        if (v == 1 || v == 2 || v == 4 || v == 8) epw = v;
+    if (w->hbm) {
+        L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec);
+    } else {
+        for (int cand : {8, 4, 2}) {
+            if (w->hash) break;  // the spatial hash runs one environment per workgroup
+            if (w->M > max_contacts_for(cand)) continue;
+            if ((size_t)ML.bytes + (size_t)L.bytes * cand > 64 * 1024) continue;
+            if ((w->E + cand - 1) / cand < 1024) continue;
+            epw = cand;
+            break;
+        }
+        if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) {
+            int v = std::atoi(env);
+            if ((v == 1 || v == 2 || v == 4 || v == 8) && !w->hash && (size_t)ML.bytes + (size_t)L.bytes * v <= max_lds_per_workgroup(w->device)) epw = v;
+        }
     }
     if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
-    if ((size_t)ML.bytes + (size_t)L.bytes * epw > max_lds_per_workgroup(w->device)) {
-        err = "per-environment working set exceeds the LDS budget";
-        delete w;
-        return nullptr;
-    }
+    w->lds = L;
     w->epw = epw;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
@@ -241,13 +248,16 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     if ((e = dalloc(w, &w->d_con, (size_t)w->E * std::max<uint32_t>(w->M, 1))) != hipSuccess) return fail("hipMalloc", e);
     if ((e = dalloc(w, &w->d_counts, w->E)) != hipSuccess) return fail("hipMalloc", e);
     if ((e = dalloc(w, &w->d_pcounts, w->E)) != hipSuccess) return fail("hipMalloc", e);
+    if (w->hash && (e = dalloc(w, &w->d_cell_ids, (size_t)w->E * m.num_geoms)) != hipSuccess) return fail("hipMalloc", e);
+    if (w->hbm && (e = dalloc(w, &w->d_work, (size_t)w->E * w->lds.bytes)) != hipSuccess) return fail("hipMalloc", e);
     struct Z { void* p; size_t n; } zeros[] = {
         {w->d_pos, EB * 16}, {w->d_quat, EB * 16}, {w->d_vel, EB * 16}, {w->d_angvel, EB * 16}, {w->d_acc, EB * 16},
         {w->d_jpos, (size_t)w->E * w->Jp * 4}, {w->d_jvel, (size_t)w->E * w->Jp * 4}, {w->d_jtrq, (size_t)w->E * w->Jp * 4},
         {w->d_obs, (size_t)w->E * w->obsp * 4}, {w->d_lam, (size_t)w->E * std::max<uint32_t>(w->N, 1) * 4},
         {w->d_actions, (size_t)w->E * w->Ap * 4}, {w->d_con, (size_t)w->E * std::max<uint32_t>(w->M, 1) * 64},
-        {w->d_counts, (size_t)w->E * 4}, {w->d_pcounts, (size_t)w->E * 4}};
-    for (const Z& z : zeros) if ((e = hipMemsetAsync(z.p, 0, z.n, w->stream)) != hipSuccess) return fail("hipMemset", e);
+        {w->d_counts, (size_t)w->E * 4}, {w->d_pcounts, (size_t)w->E * 4},
+        {w->d_cell_ids, w->d_cell_ids ? (size_t)w->E * m.num_geoms * 4 : 0}};
+    for (const Z& z : zeros) if (z.n && (e = hipMemsetAsync(z.p, 0, z.n, w->stream)) != hipSuccess) return fail("hipMemset", e);
     // initializeState (world.zig:663-691): every env starts from the scene pose.
     hipLaunchKernelGGL(reset_envs_kernel, dim3(blocks_for((uint64_t)w->E * (w->B + w->J), 256)), dim3(256), 0, w->stream,
                        w->E, w->B, w->J, w->Jp, (const uint8_t*)nullptr, w->d_init_pos, w->d_init_quat, w->d_init_vel,
@@ -288,6 +298,9 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     StepArgs a{};
     a.E = E; a.B = B; a.J = J; a.Jp = Jp; a.A = A; a.S = model.num_sensors; a.obsp = obsp; a.N = N;
     a.nrec = nrec; a.njph = njph; a.M = M; a.P = model.num_pairs;
+    a.G = model.num_geoms; a.Gp = hash ? hash_pad(model.num_geoms) : 0; a.hash = hash ? 1u : 0u;
+    a.cell_ids = d_cell_ids;
+    a.work = d_work;
     a.iters = iters; a.substeps = substeps;
     a.dt = dt;
     a.inv_step = timestep > 0 ? 1.0f / timestep : 0.0f;

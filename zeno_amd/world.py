@@ -377,6 +377,21 @@ class ZenoWorld:
         self._lib.zeno_amd_world_launch_config(self._handle, C.byref(epw), C.byref(lds))
         return epw.value, lds.value
 
+    def modes(self) -> Dict[str, bool]:
+        """{"hbm": working sets in HBM, "spatial_hash": spatial-hash broad phase (G > 512)}."""
+        hbm = C.c_int()
+        sh = C.c_int()
+        self._lib.zeno_amd_world_modes(self._handle, C.byref(hbm), C.byref(sh))
+        return {"hbm": bool(hbm.value), "spatial_hash": bool(sh.value)}
+
+    def get_cell_ids(self) -> np.ndarray:
+        """[num_envs, num_geoms] spatial-hash cell of each geom in the last substep."""
+        out = np.zeros((self._num_envs, self.num_geoms), dtype=np.uint32)
+        rc = self._lib.zeno_amd_world_get_cell_ids(self._handle, out.ctypes.data_as(C.POINTER(C.c_uint32)))
+        if rc != 0:
+            raise RuntimeError(f"get_cell_ids failed: {rc} (the scene does not use the spatial hash?)")
+        return out
+
     def model_view(self) -> Dict[str, Any]:
         from .model import view_to_dict
         v = L.ZenoAmdModelView()
