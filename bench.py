@@ -104,11 +104,13 @@ def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
 
 
 def main() -> int:
+    from zeno_amd.scenes import WORKLOADS, workload_inputs
+
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="ant", choices=["pendulum", "cartpole", "ant", "humanoid", "pile"])
+    ap.add_argument("--workload", default="ant", choices=sorted(WORKLOADS))
     ap.add_argument("--envs", type=int, default=0, help="override the workload's env count")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
@@ -125,7 +127,6 @@ def main() -> int:
               "traffic, and this build targets a single MI355X. Run with --gpus 1.", file=sys.stderr)
         return 2
 
-    from zeno_amd.scenes import WORKLOADS, workload_inputs
     from zeno_amd.world import ZenoWorld
 
     wl = WORKLOADS[args.workload]

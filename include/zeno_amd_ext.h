@@ -88,11 +88,14 @@ int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, ui
  * per workgroup (0 when the working sets live in HBM). */
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
 
-/* *hbm = 1 when the environments' working sets live in HBM (a scene whose model records
- * plus one working set exceed a workgroup's LDS, or ZENO_AMD_WORKING_SET=hbm at create);
+/* *placement: where the step kernel keeps the scene's model records and each environment's
+ * working set. 0 = both in LDS (several environments per workgroup); 1 = model records read
+ * from HBM, working set in LDS; 2 = both in HBM. The world picks the one that keeps the
+ * most environments resident on the GPU (HIP occupancy query); ZENO_AMD_PLACEMENT=0/1/2
+ * at create forces one.
  * *spatial_hash = 1 when the scene has more than 512 geoms and the spatial-hash broad
  * phase runs (world.zig:534, all_shaders.metal:541-703). Either pointer may be null. */
-int zeno_amd_world_modes(ZenoWorldHandle world, int* hbm, int* spatial_hash);
+int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash);
 
 /* The spatial hash's cell of every geom in the last substep, [E*G] u32: x + 64 y + 4096 z
  * of the clamped unit-cell coordinates, the reference's cell_ids buffer

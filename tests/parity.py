@@ -78,12 +78,13 @@ def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, ato
 
 def make_pair(name: str, num_envs: int, steps: int, seed: int = 0, envs_per_wave: Optional[int] = None,
               substeps: int = 1, max_contacts: int = 64, contact_iterations: int = 4,
-              working_set: Optional[str] = None):
-    """GPU world and oracle on the same seeded state. envs_per_wave / working_set ("hbm")
-    override the launch shape the world would choose."""
+              placement: Optional[int] = None):
+    """GPU world and oracle on the same seeded state. envs_per_wave / placement (1: model
+    records in HBM, 2: working sets in HBM too) override the launch shape the world would
+    choose."""
     path, xml, model, state, acts = workload_inputs(name, num_envs, steps, seed)
     overrides = {"ZENO_AMD_ENVS_PER_WAVE": None if envs_per_wave is None else str(envs_per_wave),
-                 "ZENO_AMD_WORKING_SET": working_set}
+                 "ZENO_AMD_PLACEMENT": None if placement is None else str(placement)}
     saved = {k: os.environ.get(k) for k in overrides}
     try:
         for k, v in overrides.items():

@@ -1,10 +1,10 @@
 """Spatial-hash broad phase (scenes above 512 geoms, world.zig:534) and working sets in HBM,
 on the GPU against the CPU oracle through the C ABI.
 
-hash_terrain (521 geoms, 9 bodies) runs the hash with its working set in LDS; pile_hash
-(601 geoms and bodies) is too large for LDS and runs the hash with its working set in HBM.
-Ant and Humanoid forced into HBM working sets check that path against the LDS one's
-oracle. Discrete outputs, including each geom's hash cell, are bit-exact; fp32 state
+hash_terrain (521 geoms, 9 bodies) runs the hash with the model records and its working
+set in LDS; pile_hash (601 geoms and bodies) reads its model records from HBM with the
+working set in LDS, and is also forced to keep the working set in HBM. Ant, Humanoid and
+the 64-body pile forced into each larger-scene placement check those paths. Discrete outputs, including each geom's hash cell, are bit-exact; fp32 state
 within the contact-rich tolerance of the other multi-step tests.
 """
 import numpy as np
@@ -15,10 +15,12 @@ from tests.parity import compare, gpu_arrays, make_pair, oracle_arrays
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name,envs,steps,hbm", [("hash_terrain", 16, 40, False), ("pile_hash", 8, 12, True)])
-def test_spatial_hash_parity(name, envs, steps, hbm):
-    g, o, acts = make_pair(name, envs, steps, seed=3)
-    assert g.modes() == {"hbm": hbm, "spatial_hash": True}
+@pytest.mark.parametrize("name,envs,steps,force,placement", [("hash_terrain", 16, 40, None, 0),
+                                                              ("pile_hash", 8, 12, None, 1),
+                                                              ("pile_hash", 4, 6, 2, 2)])
+def test_spatial_hash_parity(name, envs, steps, force, placement):
+    g, o, acts = make_pair(name, envs, steps, seed=3, placement=force)
+    assert g.modes() == {"placement": placement, "spatial_hash": True}
     G = g.num_geoms
     worst = {}
     for k in range(steps):
@@ -32,11 +34,13 @@ def test_spatial_hash_parity(name, envs, steps, hbm):
     print(name, "worst |diff| over", steps, "steps:", worst)
 
 
+@pytest.mark.parametrize("placement", [1, 2])
 @pytest.mark.parametrize("name,envs,steps", [("ant", 16, 20), ("humanoid", 8, 20), ("pile", 4, 10)])
-def test_hbm_working_set_parity(name, envs, steps):
-    g, o, acts = make_pair(name, envs, steps, seed=9, working_set="hbm")
-    assert g.modes() == {"hbm": True, "spatial_hash": False}
-    assert g.launch_config() == (1, 0)
+def test_placement_parity(name, envs, steps, placement):
+    g, o, acts = make_pair(name, envs, steps, seed=9, placement=placement)
+    assert g.modes() == {"placement": placement, "spatial_hash": False}
+    epw, lds = g.launch_config()
+    assert epw == 1 and (lds == 0) == (placement == 2)
     for k in range(steps):
         g.step(acts[k])
         o.step(acts[k])

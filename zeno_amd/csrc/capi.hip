@@ -415,13 +415,16 @@ int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave,
     if (!world) return ZENO_INVALID_HANDLE;
     const World* w = W(world);
     if (envs_per_wave) *envs_per_wave = (uint32_t)w->epw;
-    if (lds_bytes) *lds_bytes = w->hbm ? 0u : w->ml.bytes + w->lds.bytes * (uint32_t)w->epw;
+    if (lds_bytes) {
+        *lds_bytes = w->placement == za::PL_ALL_HBM ? 0u
+                   : w->lds.bytes * (uint32_t)w->epw + (w->placement == za::PL_LDS ? w->ml.bytes : 0u);
+    }
     return ZENO_SUCCESS;
 }
 
-int zeno_amd_world_modes(ZenoWorldHandle world, int* hbm, int* spatial_hash) {
+int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash) {
     if (!world) return ZENO_INVALID_HANDLE;
-    if (hbm) *hbm = W(world)->hbm ? 1 : 0;
+    if (placement) *placement = (int)W(world)->placement;
     if (spatial_hash) *spatial_hash = W(world)->hash ? 1 : 0;
     return ZENO_SUCCESS;
 }

@@ -30,7 +30,7 @@ struct EnvLds {
     // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom).
     uint32_t hkey, hcell;
     // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
-    // when the working set lives in HBM (the model blob is then read in place).
+    // when the model blob is read in place from HBM.
     uint32_t jrec;
     uint32_t last;                                                     // u16[B]
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
@@ -244,11 +244,16 @@ struct StepArgs {
     // Optional per-phase wall-clock ticks of workgroup 0 (profiling); null when unused.
     unsigned long long* phase_ticks; // [kPhaseCount]
     uint32_t* cell_ids;             // [E*G] hash mode: each geom's cell in the last substep
-    // Working sets in HBM (scenes whose working set exceeds LDS): lds.bytes per
-    // environment, one environment per workgroup. Null: working sets in LDS.
-    unsigned char* work;
+    uint32_t placement;             // Placement of the model records and working sets
+    unsigned char* work;            // PL_ALL_HBM: lds.bytes per environment; else null
     EnvLds lds;
 };
+
+// Where the step kernel keeps the model records and each environment's working set.
+// PL_LDS: both in LDS (several environments per workgroup). PL_MODEL_HBM: the model blob
+// is read in place from HBM (through the caches) and the working set is in LDS.
+// PL_ALL_HBM: both in HBM. The world picks the first that fits a workgroup's LDS.
+enum Placement : uint32_t { PL_LDS = 0, PL_MODEL_HBM = 1, PL_ALL_HBM = 2 };
 
 // Phases timed by the kernel when profiling is enabled.
 enum Phase { PH_LOAD, PH_FORCES, PH_BROAD, PH_NARROW, PH_JOINTS, PH_CONTACTS, PH_POST, PH_STORE, kPhaseCount };
@@ -256,8 +261,12 @@ enum Phase { PH_LOAD, PH_FORCES, PH_BROAD, PH_NARROW, PH_JOINTS, PH_CONTACTS, PH
 // Largest dynamic LDS allocation one workgroup may request on `device`.
 size_t max_lds_per_workgroup(int device);
 
+// Step-kernel workgroups one CU holds at once for a launch shape (LDS and register
+// limits, from the HIP occupancy query); 0 when the shape cannot launch.
+int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem);
+
 // Launches ceil(E / envs_per_wave) single-wave workgroups. envs_per_wave in {1,2,4,8};
-// 1 when a.work is set (working sets in HBM).
+// 1 unless a.placement is PL_LDS and the hash is off.
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream);
 
 // Largest M supported for a given envs_per_wave (the sort and the contact schedule keep

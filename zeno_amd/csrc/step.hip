@@ -42,7 +42,7 @@ struct Lds {
     float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
     uint16_t *order, *vlist, *lst, *loff, *last;
     uint32_t *hkey, *hcell;  // spatial hash, aliased on skey
-    float4* jrec;            // per-environment solve records (HBM working sets)
+    float4* jrec;            // per-environment solve records (model records in HBM)
     uint32_t* misc;
 };
 
@@ -516,7 +516,7 @@ __device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, Cont
 // world.zig:534). The reference's dense per-env grid (64^3 counters and offsets, a serial
 // 262,144-cell scan per env) becomes a sorted list: every geom's key cell << 14 | geom is
 // sorted in the env's working set, and a geom's 3x3x3 neighbourhood is nine rows of three
-// consecutive cell ids, each found by binary search. Appends follow the sequential order
+// consecutive cell ids, each found by one binary search and read forward. Appends follow the sequential order
 // of the reference's loops: geom ascending, then dz, dy, dx, then geoms of a cell in
 // ascending order (the reference's atomic appends make any interleaving possible).
 // ---------------------------------------------------------------------------------------
@@ -526,7 +526,7 @@ __device__ __forceinline__ uint32_t hash_axis(float p) {
     return !(f >= 0.0f) ? 0u : (f >= 63.0f ? 63u : (uint32_t)f);
 }
 
-// First position in key[0, n) whose cell is >= cell.
+// First position in key[lo, n) whose cell is >= cell.
 __device__ __forceinline__ uint32_t hash_lower_bound(const uint32_t* key, uint32_t lo, uint32_t n, uint32_t cell) {
     uint32_t hi = n;
     while (lo < hi) {
@@ -555,10 +555,11 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
             const int ny = cy + dy;
             if (ny < 0 || ny > 63) continue;
             const uint32_t row = (uint32_t)ny * 64u + (uint32_t)nz * 4096u;
-            uint32_t k = hash_lower_bound(s.hkey, 0, a.G, row + xlo);
-            const uint32_t end = hash_lower_bound(s.hkey, k, a.G, row + xhi + 1u);
-            for (; k < end; ++k) {
-                const uint32_t o = s.hkey[k] & 0x3FFFu;
+            const uint32_t last = (row + xhi) << 14 | 0x3FFFu;  // largest key of the row's cells
+            for (uint32_t k = hash_lower_bound(s.hkey, 0, a.G, row + xlo); k < a.G; ++k) {
+                const uint32_t key = s.hkey[k];
+                if (key > last) break;
+                const uint32_t o = key & 0x3FFFu;
                 if (o <= g) continue;
                 const GeomRec& gb = md.geoms[o];
                 const uint32_t body_b = gb.type_body[1];
@@ -581,15 +582,17 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
     return hits;
 }
 
-// HBM = false: the model records and EPW working sets live in LDS. HBM = true (EPW 1):
-// the working set lives in a.work and the model blob is read in place, for scenes whose
-// working set does not fit in LDS.
-// HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms, one environment
-// per workgroup) instead of the candidate pair list.
-template <int EPW, bool HBM, bool HASH>
+// PL: where the model records and the working sets live (Placement): PL_LDS, both in LDS
+// (EPW environments per workgroup); PL_MODEL_HBM, the model blob read in place from HBM
+// and one working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work).
+// HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms) instead of the
+// candidate pair list. Both non-LDS placements and the hash run one environment per
+// workgroup.
+template <int EPW, int PL, bool HASH>
 __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
-    static_assert(!HBM || EPW == 1, "HBM working sets run one environment per workgroup");
+    constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
+    static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
@@ -597,10 +600,11 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     const int sl = tid % G;
     const uint32_t env = blockIdx.x * EPW + le;
     const bool live = env < a.E;
-    unsigned char* const env_base = HBM ? a.work + (size_t)blockIdx.x * a.lds.bytes : smem + a.ml.bytes;
+    unsigned char* const env_base = HBM ? a.work + (size_t)blockIdx.x * a.lds.bytes
+                                        : smem + (PL == PL_LDS ? a.ml.bytes : 0u);
     const Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
-    Mdl md = bind_model(HBM ? (const unsigned char*)a.model : smem, a.ml);
-    if (HBM) md.jrec = s.jrec;
+    Mdl md = bind_model(PL == PL_LDS ? smem : (const unsigned char*)a.model, a.ml);
+    if (PL != PL_LDS) md.jrec = s.jrec;
     const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
     const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
 
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     };
 
     // ---- Model records (one blob per scene) -> LDS -------------------------------------
-    if (!HBM) {
+    if (PL == PL_LDS) {
         for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
     } else {
         const uint4* src = a.model + a.ml.jrec / 16u;
@@ -1180,14 +1184,29 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         if (_e != hipSuccess) return _e; \
     } while (0)
 
-template <int EPW, bool HASH>
+template <int EPW, int PL, bool HASH>
 hipError_t allow_lds(size_t shmem) {
     // Workgroups above 64 KB of dynamic LDS must opt in per kernel (gfx950 has 160 KB / CU).
     static size_t granted = 64 * 1024;
     if (shmem <= granted) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, false, HASH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, PL, HASH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e == hipSuccess) granted = shmem;
     return e;
+}
+
+template <int EPW, int PL, bool HASH>
+int resident_as(size_t shmem) {
+    if (allow_lds<EPW, PL, HASH>(shmem) != hipSuccess) return 0;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH>, kWave, shmem) != hipSuccess) return 0;
+    return n;
+}
+
+template <int EPW, int PL, bool HASH>
+hipError_t launch_as(const StepArgs& a, uint32_t blocks, size_t shmem, hipStream_t stream) {
+    ZA_CHECK((allow_lds<EPW, PL, HASH>(shmem)));
+    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH>), dim3(blocks), dim3(kWave), shmem, stream, a);
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -1198,36 +1217,49 @@ size_t max_lds_per_workgroup(int device) {
     return (size_t)v;
 }
 
+int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem) {
+    if (hash || placement != PL_LDS) {
+        if (envs_per_wave != 1) return 0;
+        switch (placement) {
+            case PL_LDS: return resident_as<1, PL_LDS, true>(shmem);
+            case PL_MODEL_HBM: return hash ? resident_as<1, PL_MODEL_HBM, true>(shmem) : resident_as<1, PL_MODEL_HBM, false>(shmem);
+            case PL_ALL_HBM: return hash ? resident_as<1, PL_ALL_HBM, true>(0) : resident_as<1, PL_ALL_HBM, false>(0);
+            default: return 0;
+        }
+    }
+    switch (envs_per_wave) {
+        case 1: return resident_as<1, PL_LDS, false>(shmem);
+        case 2: return resident_as<2, PL_LDS, false>(shmem);
+        case 4: return resident_as<4, PL_LDS, false>(shmem);
+        case 8: return resident_as<8, PL_LDS, false>(shmem);
+        default: return 0;
+    }
+}
+
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
     if (a.E == 0) return hipSuccess;
     const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
-    if ((a.work != nullptr || a.hash) && envs_per_wave != 1) return hipErrorInvalidValue;
-    if (a.work != nullptr) {
-        if (a.hash) hipLaunchKernelGGL((step_kernel<1, true, true>), dim3(blocks), dim3(kWave), 0, stream, a);
-        else hipLaunchKernelGGL((step_kernel<1, true, false>), dim3(blocks), dim3(kWave), 0, stream, a);
-        return hipGetLastError();
-    }
-    const size_t shmem = (size_t)a.ml.bytes + (size_t)a.lds.bytes * (size_t)envs_per_wave;
-    if (a.hash) {
-        ZA_CHECK((allow_lds<1, true>(shmem)));
-        hipLaunchKernelGGL((step_kernel<1, false, true>), dim3(blocks), dim3(kWave), shmem, stream, a);
-        return hipGetLastError();
-    }
-    switch (envs_per_wave) {
-        case 1: ZA_CHECK((allow_lds<1, false>(shmem))); break;
-        case 2: ZA_CHECK((allow_lds<2, false>(shmem))); break;
-        case 4: ZA_CHECK((allow_lds<4, false>(shmem))); break;
-        case 8: ZA_CHECK((allow_lds<8, false>(shmem))); break;
+    if ((a.placement != PL_LDS || a.hash) && envs_per_wave != 1) return hipErrorInvalidValue;
+    if ((a.placement == PL_ALL_HBM) != (a.work != nullptr)) return hipErrorInvalidValue;
+    const size_t env_lds = (size_t)a.lds.bytes * (size_t)envs_per_wave;
+    switch (a.placement) {
+        case PL_ALL_HBM:
+            return a.hash ? launch_as<1, PL_ALL_HBM, true>(a, blocks, 0, stream) : launch_as<1, PL_ALL_HBM, false>(a, blocks, 0, stream);
+        case PL_MODEL_HBM:
+            return a.hash ? launch_as<1, PL_MODEL_HBM, true>(a, blocks, env_lds, stream)
+                          : launch_as<1, PL_MODEL_HBM, false>(a, blocks, env_lds, stream);
+        case PL_LDS: break;
         default: return hipErrorInvalidValue;
     }
+    const size_t shmem = (size_t)a.ml.bytes + env_lds;
+    if (a.hash) return launch_as<1, PL_LDS, true>(a, blocks, shmem, stream);
     switch (envs_per_wave) {
-        case 1: hipLaunchKernelGGL((step_kernel<1, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 2: hipLaunchKernelGGL((step_kernel<2, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 4: hipLaunchKernelGGL((step_kernel<4, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
-        case 8: hipLaunchKernelGGL((step_kernel<8, false, false>), dim3(blocks), dim3(kWave), shmem, stream, a); break;
+        case 1: return launch_as<1, PL_LDS, false>(a, blocks, shmem, stream);
+        case 2: return launch_as<2, PL_LDS, false>(a, blocks, shmem, stream);
+        case 4: return launch_as<4, PL_LDS, false>(a, blocks, shmem, stream);
+        case 8: return launch_as<8, PL_LDS, false>(a, blocks, shmem, stream);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace za

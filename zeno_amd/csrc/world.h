@@ -31,7 +31,7 @@ struct World {
     int epw = 1;
     EnvLds lds{};
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
-    bool hbm = false;   // working sets in HBM (d_work) instead of LDS
+    uint32_t placement = PL_LDS;  // where the step kernel keeps model records and working sets
     hipStream_t stream = nullptr;
     size_t device_bytes = 0;
 

@@ -165,30 +165,60 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->nrec = (uint32_t)(jrec.size() / kJRecQuads);
     w->njph = (uint32_t)jph.size();
     const ModelLayout ML = make_model_layout(w->B, w->J, m.num_geoms, m.num_pairs, w->A, m.num_sensors, w->nrec, w->njph);
-    // Launch shape: the largest environments-per-wave that keeps at least ~one wave per
-    // SIMD (1024 on MI355X), fits the sort's register budget and 64 KB of LDS. A scene
-    // whose model records plus one working set exceed the workgroup's LDS keeps its
-    // working sets in HBM instead (one environment per wave); ZENO_AMD_WORKING_SET=hbm
-    // selects that path for any scene.
-    const char* ws = std::getenv("ZENO_AMD_WORKING_SET");
-    w->hbm = (ws && std::strcmp(ws, "hbm") == 0) || (size_t)ML.bytes + (size_t)L.bytes > max_lds_per_workgroup(w->device);
-    int epw = 1;
-    if (w->hbm) {
-        L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec);
-    } else {
+    // Placement and launch shape. The step is a chain of dependent solver phases per
+    // environment, so throughput follows the number of environments a CU holds at once:
+    // each candidate (model records and working sets in LDS with 1, 2, 4 or 8 environments
+    // per wave; model records read from HBM with one working set in LDS; both in HBM) is
+    // scored by min(E, environments resident on the GPU), from the HIP occupancy query
+    // (LDS and registers). Ties keep the earlier candidate: LDS before HBM, and among the
+    // LDS shapes first the largest environments-per-wave with at least 1024 workgroups
+    // and 64 KB of LDS, then the others from 1 up. ZENO_AMD_PLACEMENT=0/1/2 and
+    // ZENO_AMD_ENVS_PER_WAVE force a placement or a shape (tests of each path; a forced
+    // shape implies placement 0).
+    const size_t lds_max = max_lds_per_workgroup(w->device);
+    int cus = 256;
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
+    const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec);
+    struct Cand { uint32_t pl; int epw; size_t shmem; };
+    std::vector<Cand> cands;
+    int force_pl = -1, force_epw = 0;
+    if (const char* env = std::getenv("ZENO_AMD_PLACEMENT")) force_pl = std::min(std::max(std::atoi(env), 0), 2);
+    if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) force_epw = std::atoi(env);
+    if (force_epw > 0 && force_pl < 0) force_pl = PL_LDS;
+    {
+        std::vector<int> order;
         for (int cand : {8, 4, 2}) {
-            if (w->hash) break;  // the spatial hash runs one environment per workgroup
-            if (w->M > max_contacts_for(cand)) continue;
+            if (w->hash || w->M > max_contacts_for(cand)) continue;
             if ((size_t)ML.bytes + (size_t)L.bytes * cand > 64 * 1024) continue;
             if ((w->E + cand - 1) / cand < 1024) continue;
-            epw = cand;
+            order.push_back(cand);
             break;
         }
-        if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) {
-            int v = std::atoi(env);
-            if ((v == 1 || v == 2 || v == 4 || v == 8) && !w->hash && (size_t)ML.bytes + (size_t)L.bytes * v <= max_lds_per_workgroup(w->device)) epw = v;
+        for (int cand : {1, 2, 4, 8}) {
+            if (cand > 1 && (w->hash || w->M > max_contacts_for(cand))) continue;
+            if (std::find(order.begin(), order.end(), cand) == order.end()) order.push_back(cand);
         }
+        for (int cand : order) {
+            const size_t shmem = (size_t)ML.bytes + (size_t)L.bytes * cand;
+            if (shmem <= lds_max) cands.push_back({PL_LDS, cand, shmem});
+        }
+        if ((size_t)L_own.bytes <= lds_max) cands.push_back({PL_MODEL_HBM, 1, (size_t)L_own.bytes});
+        cands.push_back({PL_ALL_HBM, 1, 0});
     }
+    const Cand* best = nullptr;
+    uint64_t best_score = 0;
+    for (const Cand& c : cands) {
+        if (force_pl >= 0 && (int)c.pl != force_pl) continue;
+        if (force_epw > 0 && c.epw != force_epw) continue;
+        const int n = resident_workgroups(c.epw, c.pl, w->hash, c.shmem);
+        if (n <= 0) continue;
+        const uint64_t score = std::min<uint64_t>(w->E, (uint64_t)n * (uint64_t)c.epw * (uint64_t)cus);
+        if (!best || score > best_score) { best = &c; best_score = score; }
+    }
+    if (!best) { err = "no launch shape fits this scene (ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE?)"; delete w; return nullptr; }
+    w->placement = best->pl;
+    const int epw = best->epw;
+    if (best->pl != PL_LDS) L = L_own;
     if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
     w->lds = L;
     w->epw = epw;
@@ -249,7 +279,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     if ((e = dalloc(w, &w->d_counts, w->E)) != hipSuccess) return fail("hipMalloc", e);
     if ((e = dalloc(w, &w->d_pcounts, w->E)) != hipSuccess) return fail("hipMalloc", e);
     if (w->hash && (e = dalloc(w, &w->d_cell_ids, (size_t)w->E * m.num_geoms)) != hipSuccess) return fail("hipMalloc", e);
-    if (w->hbm && (e = dalloc(w, &w->d_work, (size_t)w->E * w->lds.bytes)) != hipSuccess) return fail("hipMalloc", e);
+    if (w->placement == PL_ALL_HBM && (e = dalloc(w, &w->d_work, (size_t)w->E * w->lds.bytes)) != hipSuccess) return fail("hipMalloc", e);
     struct Z { void* p; size_t n; } zeros[] = {
         {w->d_pos, EB * 16}, {w->d_quat, EB * 16}, {w->d_vel, EB * 16}, {w->d_angvel, EB * 16}, {w->d_acc, EB * 16},
         {w->d_jpos, (size_t)w->E * w->Jp * 4}, {w->d_jvel, (size_t)w->E * w->Jp * 4}, {w->d_jtrq, (size_t)w->E * w->Jp * 4},
@@ -300,6 +330,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.nrec = nrec; a.njph = njph; a.M = M; a.P = model.num_pairs;
     a.G = model.num_geoms; a.Gp = hash ? hash_pad(model.num_geoms) : 0; a.hash = hash ? 1u : 0u;
     a.cell_ids = d_cell_ids;
+    a.placement = placement;
     a.work = d_work;
     a.iters = iters; a.substeps = substeps;
     a.dt = dt;

@@ -377,12 +377,13 @@ class ZenoWorld:
         self._lib.zeno_amd_world_launch_config(self._handle, C.byref(epw), C.byref(lds))
         return epw.value, lds.value
 
-    def modes(self) -> Dict[str, bool]:
-        """{"hbm": working sets in HBM, "spatial_hash": spatial-hash broad phase (G > 512)}."""
-        hbm = C.c_int()
+    def modes(self) -> Dict[str, Any]:
+        """{"placement": 0 model + working sets in LDS, 1 model in HBM and working set in LDS,
+        2 both in HBM; "spatial_hash": the spatial-hash broad phase runs (G > 512)}."""
+        pl = C.c_int()
         sh = C.c_int()
-        self._lib.zeno_amd_world_modes(self._handle, C.byref(hbm), C.byref(sh))
-        return {"hbm": bool(hbm.value), "spatial_hash": bool(sh.value)}
+        self._lib.zeno_amd_world_modes(self._handle, C.byref(pl), C.byref(sh))
+        return {"placement": pl.value, "spatial_hash": bool(sh.value)}
 
     def get_cell_ids(self) -> np.ndarray:
         """[num_envs, num_geoms] spatial-hash cell of each geom in the last substep."""
