@@ -103,6 +103,89 @@ def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
     }
 
 
+def collide_pairs_inputs(n: int, seed: int = 0):
+    """n operand pairs for the extended narrow phase: types uniform over sphere, capsule, box
+    and plane on both sides, sizes U[0.05, 0.6], positions U[-0.7, 0.7]^3 (about a third of
+    the pairs touch), random rotations."""
+    from zeno_amd.collision import COLLIDER_DTYPE
+
+    rng = np.random.default_rng(seed)
+    sides = []
+    for _ in range(2):
+        r = np.zeros(n, COLLIDER_DTYPE)
+        r["type"] = rng.integers(0, 4, n)
+        r["size"] = rng.uniform(0.05, 0.6, (n, 3))
+        r["position"][:, :3] = rng.uniform(-0.7, 0.7, (n, 3))
+        q = rng.normal(size=(n, 4))
+        r["quaternion"] = q / np.linalg.norm(q, axis=1, keepdims=True)
+        sides.append(r)
+    return sides[0], sides[1]
+
+
+def bench_collide(n: int, steps: int, warmup: int, cpu_seconds: float, no_cpu: bool) -> dict:
+    """zeno_amd_detect_collisions over n resident pairs: HIP events on the null stream around
+    each launch; 192 algorithmic bytes per pair (two 64-B operands read, one 64-B result
+    written)."""
+    from zeno_amd import _lib as L
+    from zeno_amd.collision import CONTACT_RESULT_DTYPE
+
+    a, b = collide_pairs_inputs(n)
+    hip = C.CDLL("libamdhip64.so")
+    pa, fa = hip_device_buffer(a)
+    pb, fb = hip_device_buffer(b)
+    po, fo = hip_device_buffer(np.zeros(n, CONTACT_RESULT_DTYPE))
+    lib = L.load()
+    ev = [C.c_void_p() for _ in range(2 * steps)]
+    for e in ev:
+        hip.hipEventCreate(C.byref(e))
+    for _ in range(warmup):
+        if lib.zeno_amd_detect_collisions(C.c_void_p(pa), C.c_void_p(pb), n, C.c_void_p(po), None) != 0:
+            raise RuntimeError("detect_collisions failed")
+    hip.hipDeviceSynchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        hip.hipEventRecord(ev[2 * k], None)
+        lib.zeno_amd_detect_collisions(C.c_void_p(pa), C.c_void_p(pb), n, C.c_void_p(po), None)
+        hip.hipEventRecord(ev[2 * k + 1], None)
+    hip.hipDeviceSynchronize()
+    elapsed = time.perf_counter() - t0
+    ms = C.c_float()
+    total_ms = 0.0
+    for k in range(steps):
+        hip.hipEventElapsedTime(C.byref(ms), ev[2 * k], ev[2 * k + 1])
+        total_ms += ms.value
+    for e in ev:
+        hip.hipEventDestroy(e)
+    fa(); fb(); fo()
+    kernel_s = total_ms / 1e3 / steps
+    achieved = 192.0 * n / kernel_s / 1e9
+    result = {
+        "metric": "contact pairs/sec (narrow_phase.detectCollision, batched)",
+        "value": n * steps / elapsed, "unit": "pairs/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": 1e3 * elapsed / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic: uniform random type pairs, sizes, poses (seed 0)",
+        "config": {"workload": f"collide_pairs {n} pairs per launch (operands resident in HBM)", "pairs": n},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None, "kernel": "detect_collisions_kernel",
+                     "kernel_avg_us": kernel_s * 1e6, "algorithmic_bytes_per_pair": 192,
+                     "algorithmic_bytes_per_launch": 192 * n},
+    }
+    if not no_cpu:
+        from oracle.oracle import detect_collisions as cpu_detect
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+        m = min(n, 1 << 20)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds:
+            cpu_detect(a[:m], b[:m], nthreads=threads)
+            done += m
+        dt = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": done / dt, "unit": "pairs/s", "cores": threads, "kind": "port",
+                                  "sample": f"C oracle of detectCollision, OpenMP over pairs, {done} pairs "
+                                            f"(the first {m} of the same inputs, repeated), {dt:.1f} s"}
+    return result
+
+
 def main() -> int:
     from zeno_amd.scenes import WORKLOADS, workload_inputs
 
@@ -118,7 +201,13 @@ def main() -> int:
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run 3 device-to-device copies of this many MiB (a plain copy kernel "
                          "of known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--collide-pairs", type=int, default=0,
+                    help="instead of the step, time the batched extended narrow phase on this many pairs")
     args = ap.parse_args()
+    if args.collide_pairs > 0:
+        print(json.dumps(bench_collide(args.collide_pairs, min(args.steps, 200), max(args.warmup, 1),
+                                       min(args.cpu_seconds, 10.0), args.no_cpu)), flush=True)
+        return 0
     if args.calibrate_copy_mib > 0:
         calibrate_copy(args.calibrate_copy_mib << 20)
 

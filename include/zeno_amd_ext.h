@@ -1,13 +1,15 @@
 /*
  * zeno_amd_ext.h — extension entry points of libzeno (MI355X build).
  *
- * None of these exist in the reference (Lulzx/zeno); they sit beside the reference ABI of
- * zeno.h and serve three callers:
+ * None of these exist in the reference's C ABI (Lulzx/zeno); they sit beside the reference
+ * ABI of zeno.h and serve four callers:
  *   - inspection of the model a world was built from (tests and the CPU oracle read the
  *     constraint templates, colours and records the kernels use), without a GPU;
  *   - device-resident stepping and timing for benchmarks and graph capture;
  *   - solver state that the reference keeps but never exposes (lambda, previous contact
- *     count), used by parity tests.
+ *     count, spatial-hash cells), used by parity tests;
+ *   - the reference's Zig-level collision routine (narrow_phase.detectCollision) for C
+ *     callers, batched on the GPU.
  */
 #ifndef ZENO_AMD_EXT_H
 #define ZENO_AMD_EXT_H
@@ -102,6 +104,46 @@ int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_has
  * (world.zig:140,548; all_shaders.metal:576-582), which it keeps without a getter.
  * ZENO_INVALID_ARGUMENT when the scene does not use the spatial hash. */
 int zeno_amd_world_get_cell_ids(ZenoWorldHandle world, uint32_t* out /* [E*G] */);
+
+/* ---- Extended narrow phase ---------------------------------------------------------
+ * The reference's host-side collision routine narrow_phase.detectCollision(geom_a,
+ * transform_a, geom_b, transform_b) ?ContactResult (src/collision/narrow_phase.zig:28-123,
+ * exported through the `zeno` Zig module, src/main.zig:28; it has no C entry point there),
+ * batched on the GPU. Pairs handled: sphere-sphere, sphere-capsule, sphere-box,
+ * sphere-plane, capsule-capsule, capsule-plane, box-plane, box-box (separating axes), in
+ * either operand order; every other pair (capsule-box, cylinder, mesh, heightfield, plane-
+ * plane) reports no contact. */
+
+/* One operand: the geom's type, size and local position (primitives.Geom,
+ * primitives.zig:135-166) and its body's transform (body.Transform, body.zig:141-143).
+ * 64 bytes. */
+typedef struct {
+    uint32_t type;         /* 0 sphere, 1 capsule, 2 box, 3 plane, 4 cylinder, 5 mesh, 6 heightfield */
+    float size[3];         /* radius | radius, half length | half extents | plane offset */
+    float local_pos[4];    /* w unused */
+    float position[4];     /* w unused */
+    float quaternion[4];   /* xyzw */
+} ZenoAmdCollider;
+
+/* narrow_phase.ContactResult (narrow_phase.zig:12-25); all zero with valid = 0 where the
+ * reference returns null. 64 bytes. */
+typedef struct {
+    float point[3];
+    float penetration;
+    float normal[3];       /* from a to b */
+    uint32_t valid;
+    float local_a[4];      /* w 0 */
+    float local_b[4];      /* w 0 */
+} ZenoAmdContactResult;
+
+/* detectCollision(a[i], b[i]) -> out[i] for i < n. Device pointers; enqueued on `stream`
+ * (a hipStream_t; null = the default stream), returns after enqueueing. */
+int zeno_amd_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                               ZenoAmdContactResult* out, void* stream);
+
+/* The same on host arrays: copies in, runs on the current device, copies back, waits. */
+int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                    ZenoAmdContactResult* out);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,13 @@ CONSTRAINT_DTYPE = np.dtype([("indices", "4u4"), ("anchor_a", "4f4"), ("anchor_b
                              ("axis_target", "4f4"), ("limits", "4f4"), ("state", "4f4")])
 
 
+# narrow_phase.detectCollision operands and result (zeno_oracle.h ZoCollider / ZoContactResult)
+COLLIDER_DTYPE = np.dtype([("type", "u4"), ("size", "3f4"), ("local_pos", "4f4"), ("position", "4f4"),
+                           ("quaternion", "4f4")])
+CONTACT_RESULT_DTYPE = np.dtype([("point", "3f4"), ("penetration", "f4"), ("normal", "3f4"), ("valid", "u4"),
+                                 ("local_a", "4f4"), ("local_b", "4f4")])
+
+
 class ZoModel(C.Structure):
     _fields_ = [
         ("num_envs", C.c_uint32), ("num_bodies", C.c_uint32), ("num_joints", C.c_uint32),
@@ -65,6 +72,10 @@ def load() -> C.CDLL:
         lib.zo_match_cached.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]
         lib.zo_sort_contacts.restype = None
         lib.zo_sort_contacts.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32]
+        lib.zo_detect_collision.restype = C.c_int
+        lib.zo_detect_collision.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.zo_detect_collisions.restype = None
+        lib.zo_detect_collisions.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_int]
         lib.zo_broad_phase_hash.restype = None
         lib.zo_broad_phase_hash.argtypes = [C.POINTER(ZoModel), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         lib.zo_collide_env.restype = None
@@ -261,6 +272,18 @@ def broad_phase_hash(world: "OracleWorld", env: int = 0, count: int = 0):
     con = np.zeros(world.M, CONTACT_DTYPE)
     load().zo_broad_phase_hash(C.byref(zm), _p(np.ascontiguousarray(world.positions[env])), _p(ids), _p(con), _p(cnt))
     return ids[:G], con, int(cnt[0])
+
+
+def detect_collisions(a: np.ndarray, b: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    """narrow_phase.detectCollision for each pair (a[i], b[i]) of COLLIDER_DTYPE records;
+    returns CONTACT_RESULT_DTYPE records (all zero, valid 0, where there is no contact)."""
+    a = np.ascontiguousarray(a, COLLIDER_DTYPE)
+    b = np.ascontiguousarray(b, COLLIDER_DTYPE)
+    assert a.shape == b.shape and a.ndim == 1
+    out = np.zeros(a.shape[0], CONTACT_RESULT_DTYPE)
+    if a.shape[0]:
+        load().zo_detect_collisions(_p(a), _p(b), a.shape[0], _p(out), nthreads)
+    return out
 
 
 def atan2f(y: float, x: float) -> float:

@@ -1173,3 +1173,305 @@ uint32_t zo_build_templates(const ZoJoint* joints, const uint8_t* limited, uint3
     }
     return n;
 }
+
+/* ------------------------------------------------------------------------------------
+ * Extended narrow phase: narrow_phase.detectCollision and the primitive pairs it
+ * dispatches to (src/collision/narrow_phase.zig:28-512, helpers :786-925), with
+ * body.Transform (src/physics/body.zig:141-268) and primitives.Geom accessors
+ * (src/collision/primitives.zig:223-240,413-415). Heightfield, mesh and cylinder pairs
+ * (GJK/EPA, :513-785) are not restated: those return no contact here.
+ *
+ * Zig semantics kept: no FMA contraction, correctly rounded sqrt and division,
+ * std.math.clamp(x, lo, hi) = @max(lo, @min(x, hi)) where @min/@max return the non-NaN
+ * operand (between +0 and -0 this restatement returns the second operand), @abs = fabs.
+ * Axes come from the body transform only (a geom's own local rotation is not applied),
+ * as in the reference.
+ * ---------------------------------------------------------------------------------- */
+#define ZO_NP_EPS 1e-6f /* constants.EPSILON (src/physics/constants.zig:13) */
+
+static float np_min(float a, float b) { return a != a ? b : (b != b ? a : (a < b ? a : b)); }
+static float np_max(float a, float b) { return a != a ? b : (b != b ? a : (a > b ? a : b)); }
+static float np_clamp(float x, float lo, float hi) { return np_max(lo, np_min(x, hi)); }
+
+/* rotateByQuat, body.zig:254-264 */
+static v3 np_rot(v3 v, const float* q) {
+    v3 qv = V(q[0], q[1], q[2]);
+    v3 uv = vcross(qv, v);
+    v3 uuv = vcross(qv, uv);
+    return V(v.x + 2.0f * (q[3] * uv.x + uuv.x), v.y + 2.0f * (q[3] * uv.y + uuv.y), v.z + 2.0f * (q[3] * uv.z + uuv.z));
+}
+/* Transform.transformPoint, body.zig:192-199 */
+static v3 np_point(const ZoCollider* c, v3 local) {
+    v3 r = np_rot(local, c->quaternion);
+    return V(r.x + c->position[0], r.y + c->position[1], r.z + c->position[2]);
+}
+static v3 np_axis(const ZoCollider* c, float x, float y, float z) { return np_rot(V(x, y, z), c->quaternion); }
+
+static int np_emit(ZoContactResult* out, v3 point, v3 normal, float pen, v3 la, v3 lb) {
+    out->point[0] = point.x; out->point[1] = point.y; out->point[2] = point.z;
+    out->penetration = pen;
+    out->normal[0] = normal.x; out->normal[1] = normal.y; out->normal[2] = normal.z;
+    out->valid = 1;
+    out->local_a[0] = la.x; out->local_a[1] = la.y; out->local_a[2] = la.z; out->local_a[3] = 0.0f;
+    out->local_b[0] = lb.x; out->local_b[1] = lb.y; out->local_b[2] = lb.z; out->local_b[3] = 0.0f;
+    return 1;
+}
+
+/* flipContact, :912-920 */
+static void np_flip(ZoContactResult* r) {
+    for (int i = 0; i < 3; ++i) {
+        r->normal[i] = r->normal[i] * -1.0f;
+        float t = r->local_a[i]; r->local_a[i] = r->local_b[i]; r->local_b[i] = t;
+    }
+}
+
+/* sphereSphere, :125-153 */
+static int np_sphere_sphere(v3 pa, float ra, v3 pb, float rb, ZoContactResult* out) {
+    v3 diff = vsub(pb, pa);
+    float dist_sq = vdot(diff, diff);
+    float min_dist = ra + rb;
+    if (dist_sq >= min_dist * min_dist) return 0;
+    float dist = sqrtf(dist_sq);
+    v3 n = dist > ZO_NP_EPS ? vscale(diff, 1.0f / dist) : V(0.0f, 0.0f, 1.0f);
+    float pen = min_dist - dist;
+    v3 point = vadd(pa, vscale(n, ra - pen * 0.5f));
+    return np_emit(out, point, n, pen, vscale(n, ra), vscale(n, -rb));
+}
+
+/* closestPointOnSegment, :815-825 */
+static v3 np_closest_on_segment(v3 p, v3 s, v3 e) {
+    v3 seg = vsub(e, s);
+    float len_sq = vdot(seg, seg);
+    if (len_sq < ZO_NP_EPS) return s;
+    float t = np_clamp(vdot(vsub(p, s), seg) / len_sq, 0.0f, 1.0f);
+    return vadd(s, vscale(seg, t));
+}
+
+/* sphereCapsule, :156-197 */
+static int np_sphere_capsule(v3 sp, float sr, v3 cp, const ZoCollider* cap, ZoContactResult* out) {
+    float cr = cap->size[0], hl = cap->size[1];
+    v3 axis = np_axis(cap, 0.0f, 0.0f, 1.0f);
+    v3 p1 = vsub(cp, vscale(axis, hl));
+    v3 p2 = vadd(cp, vscale(axis, hl));
+    v3 closest = np_closest_on_segment(sp, p1, p2);
+    v3 diff = vsub(sp, closest);
+    float dist_sq = vdot(diff, diff);
+    float min_dist = sr + cr;
+    if (dist_sq >= min_dist * min_dist) return 0;
+    float dist = sqrtf(dist_sq);
+    v3 n = dist > ZO_NP_EPS ? vscale(diff, 1.0f / dist) : V(0.0f, 0.0f, 1.0f);
+    float pen = min_dist - dist;
+    v3 point = vadd(closest, vscale(n, cr - pen * 0.5f));
+    return np_emit(out, point, n, pen, vscale(n, sr), vscale(n, -cr));
+}
+
+/* spherePlane, :200-228 */
+static int np_sphere_plane(v3 sp, float sr, const ZoCollider* pl, ZoContactResult* out) {
+    v3 n = np_axis(pl, 0.0f, 0.0f, 1.0f);
+    v3 pp = np_point(pl, ld3(pl->local_pos));
+    float signed_dist = vdot(vsub(sp, pp), n) - pl->size[0];
+    if (signed_dist >= sr) return 0;
+    float pen = sr - signed_dist;
+    v3 point = vsub(sp, vscale(n, signed_dist + pen * 0.5f));
+    return np_emit(out, point, n, pen, vscale(n, -sr), V(0.0f, 0.0f, 0.0f));
+}
+
+/* boxFaceNormal, :890-910 */
+static v3 np_box_face_normal(v3 p, const float* he) {
+    float maxd = -INFINITY;
+    float pc[3] = {p.x, p.y, p.z};
+    float nrm[3] = {0.0f, 0.0f, 1.0f};
+    for (int i = 0; i < 3; ++i) {
+        float dpos = he[i] - pc[i];
+        float dneg = he[i] + pc[i];
+        if (dpos > maxd) { maxd = dpos; nrm[0] = nrm[1] = nrm[2] = 0.0f; nrm[i] = 1.0f; }
+        if (dneg > maxd) { maxd = dneg; nrm[0] = nrm[1] = nrm[2] = 0.0f; nrm[i] = -1.0f; }
+    }
+    return V(nrm[0], nrm[1], nrm[2]);
+}
+
+/* sphereBox, :231-277 (the box's inverse transform per Transform.inverse, body.zig:223-235) */
+static int np_sphere_box(v3 sp, float sr, const ZoCollider* box, ZoContactResult* out) {
+    const float* q = box->quaternion;
+    float iq[4] = {-q[0], -q[1], -q[2], q[3]};
+    v3 ipos = np_rot(V(-box->position[0], -box->position[1], -box->position[2]), iq);
+    v3 r = np_rot(sp, iq);
+    v3 ls = V(r.x + ipos.x, r.y + ipos.y, r.z + ipos.z);
+    const float* he = box->size;
+    v3 cl = V(np_clamp(ls.x, -he[0], he[0]), np_clamp(ls.y, -he[1], he[1]), np_clamp(ls.z, -he[2], he[2]));
+    v3 diff = vsub(ls, cl);
+    float dist_sq = vdot(diff, diff);
+    if (dist_sq >= sr * sr) return 0;
+    float dist = sqrtf(dist_sq);
+    v3 ln = dist > ZO_NP_EPS ? vscale(diff, 1.0f / dist) : np_box_face_normal(ls, he);
+    v3 wc = np_point(box, cl);
+    v3 n = np_rot(ln, q);
+    float pen = sr - dist;
+    v3 point = vadd(wc, vscale(n, pen * 0.5f));
+    return np_emit(out, point, n, pen, vscale(n, -sr), vsub(cl, ld3(box->local_pos)));
+}
+
+/* closestPointsBetweenSegments, :832-888 */
+static void np_closest_between_segments(v3 a1, v3 a2, v3 b1, v3 b2, v3* pa, v3* pb) {
+    v3 d1 = vsub(a2, a1), d2 = vsub(b2, b1), r = vsub(a1, b1);
+    float a = vdot(d1, d1), e = vdot(d2, d2), f = vdot(d2, r);
+    float s = 0.0f, t = 0.0f;
+    if (a < ZO_NP_EPS && e < ZO_NP_EPS) { *pa = a1; *pb = b1; return; }
+    if (a < ZO_NP_EPS) {
+        t = np_clamp(f / e, 0.0f, 1.0f);
+    } else {
+        float c = vdot(d1, r);
+        if (e < ZO_NP_EPS) {
+            s = np_clamp(-c / a, 0.0f, 1.0f);
+        } else {
+            float b = vdot(d1, d2);
+            float denom = a * e - b * b;
+            if (denom != 0.0f) s = np_clamp((b * f - c * e) / denom, 0.0f, 1.0f);
+            t = (b * s + f) / e;
+            if (t < 0.0f) {
+                t = 0.0f;
+                s = np_clamp(-c / a, 0.0f, 1.0f);
+            } else if (t > 1.0f) {
+                t = 1.0f;
+                s = np_clamp((b - c) / a, 0.0f, 1.0f);
+            }
+        }
+    }
+    *pa = vadd(a1, vscale(d1, s));
+    *pb = vadd(b1, vscale(d2, t));
+}
+
+/* capsuleCapsule, :280-331 */
+static int np_capsule_capsule(v3 pa, const ZoCollider* ca, v3 pb, const ZoCollider* cb, ZoContactResult* out) {
+    float ra = ca->size[0], rb = cb->size[0], ha = ca->size[1], hb = cb->size[1];
+    v3 xa = np_axis(ca, 0.0f, 0.0f, 1.0f), xb = np_axis(cb, 0.0f, 0.0f, 1.0f);
+    v3 a1 = vsub(pa, vscale(xa, ha)), a2 = vadd(pa, vscale(xa, ha));
+    v3 b1 = vsub(pb, vscale(xb, hb)), b2 = vadd(pb, vscale(xb, hb));
+    v3 qa, qb;
+    np_closest_between_segments(a1, a2, b1, b2, &qa, &qb);
+    v3 diff = vsub(qb, qa);
+    float dist_sq = vdot(diff, diff);
+    float min_dist = ra + rb;
+    if (dist_sq >= min_dist * min_dist) return 0;
+    float dist = sqrtf(dist_sq);
+    v3 n = dist > ZO_NP_EPS ? vscale(diff, 1.0f / dist) : V(0.0f, 0.0f, 1.0f);
+    float pen = min_dist - dist;
+    v3 wa = vadd(qa, vscale(n, ra));
+    v3 wb = vsub(qb, vscale(n, rb));
+    v3 point = vscale(vadd(wa, wb), 0.5f);
+    return np_emit(out, point, n, pen, vscale(n, ra), vscale(n, -rb));
+}
+
+/* capsulePlane, :334-370 */
+static int np_capsule_plane(v3 cp, const ZoCollider* cap, const ZoCollider* pl, ZoContactResult* out) {
+    float radius = cap->size[0], hl = cap->size[1];
+    v3 axis = np_axis(cap, 0.0f, 0.0f, 1.0f);
+    v3 n = np_axis(pl, 0.0f, 0.0f, 1.0f);
+    v3 pp = np_point(pl, ld3(pl->local_pos));
+    v3 p1 = vsub(cp, vscale(axis, hl));
+    v3 p2 = vadd(cp, vscale(axis, hl));
+    float d1 = vdot(vsub(p1, pp), n) - radius;
+    float d2 = vdot(vsub(p2, pp), n) - radius;
+    if (d1 >= 0.0f && d2 >= 0.0f) return 0;
+    v3 deepest = d1 < d2 ? p1 : p2;
+    float dist = np_min(d1, d2);
+    v3 point = vsub(deepest, vscale(n, dist * 0.5f + radius));
+    return np_emit(out, point, n, -dist, vscale(n, -radius), V(0.0f, 0.0f, 0.0f));
+}
+
+/* boxPlane, :373-423 */
+static int np_box_plane(const ZoCollider* box, const ZoCollider* pl, ZoContactResult* out) {
+    const float* h = box->size;
+    v3 n = np_axis(pl, 0.0f, 0.0f, 1.0f);
+    v3 pp = np_point(pl, ld3(pl->local_pos));
+    const float sx[8] = {-1, 1, -1, 1, -1, 1, -1, 1}, sy[8] = {-1, -1, 1, 1, -1, -1, 1, 1}, sz[8] = {-1, -1, -1, -1, 1, 1, 1, 1};
+    float min_dist = INFINITY;
+    v3 dc = V(0.0f, 0.0f, 0.0f), dw = V(0.0f, 0.0f, 0.0f);
+    for (int k = 0; k < 8; ++k) {
+        v3 corner = V(sx[k] < 0 ? -h[0] : h[0], sy[k] < 0 ? -h[1] : h[1], sz[k] < 0 ? -h[2] : h[2]);
+        v3 wc = np_point(box, corner);
+        float dist = vdot(vsub(wc, pp), n);
+        if (dist < min_dist) { min_dist = dist; dc = corner; dw = wc; }
+    }
+    if (min_dist >= 0.0f) return 0;
+    return np_emit(out, dw, n, -min_dist, dc, V(0.0f, 0.0f, 0.0f));
+}
+
+/* testAxis, :788-813; returns 0 for a separating axis */
+static int np_test_axis(v3 axis, v3 d, const v3* xa, const float* ha, const v3* xb, const float* hb, float* overlap) {
+    float proj_a = ha[0] * fabsf(vdot(axis, xa[0])) + ha[1] * fabsf(vdot(axis, xa[1])) + ha[2] * fabsf(vdot(axis, xa[2]));
+    float proj_b = hb[0] * fabsf(vdot(axis, xb[0])) + hb[1] * fabsf(vdot(axis, xb[1])) + hb[2] * fabsf(vdot(axis, xb[2]));
+    float dist = fabsf(vdot(d, axis));
+    if (dist > proj_a + proj_b) return 0;
+    *overlap = proj_a + proj_b - dist;
+    return 1;
+}
+
+/* boxBox (SAT over 15 axes), :426-512 */
+static int np_box_box(v3 pa, const ZoCollider* ba, v3 pb, const ZoCollider* bb, ZoContactResult* out) {
+    v3 xa[3] = {np_axis(ba, 1.0f, 0.0f, 0.0f), np_axis(ba, 0.0f, 1.0f, 0.0f), np_axis(ba, 0.0f, 0.0f, 1.0f)};
+    v3 xb[3] = {np_axis(bb, 1.0f, 0.0f, 0.0f), np_axis(bb, 0.0f, 1.0f, 0.0f), np_axis(bb, 0.0f, 0.0f, 1.0f)};
+    v3 d = vsub(pb, pa);
+    float min_overlap = INFINITY, ov;
+    v3 best = V(0.0f, 0.0f, 1.0f);
+    for (int i = 0; i < 3; ++i) {
+        if (!np_test_axis(xa[i], d, xa, ba->size, xb, bb->size, &ov)) return 0;
+        if (ov < min_overlap) { min_overlap = ov; best = xa[i]; }
+    }
+    for (int i = 0; i < 3; ++i) {
+        if (!np_test_axis(xb[i], d, xa, ba->size, xb, bb->size, &ov)) return 0;
+        if (ov < min_overlap) { min_overlap = ov; best = xb[i]; }
+    }
+    for (int i = 0; i < 3; ++i) {
+        for (int j = 0; j < 3; ++j) {
+            v3 edge = vcross(xa[i], xb[j]);
+            float len = sqrtf(vdot(edge, edge));
+            if (len < ZO_NP_EPS) continue;
+            v3 nrm = vscale(edge, 1.0f / len);
+            if (!np_test_axis(nrm, d, xa, ba->size, xb, bb->size, &ov)) return 0;
+            if (ov < min_overlap) { min_overlap = ov; best = nrm; }
+        }
+    }
+    if (vdot(best, d) < 0.0f) best = vscale(best, -1.0f);
+    v3 point = vadd(pa, vscale(d, 0.5f));
+    return np_emit(out, point, best, min_overlap, V(0.0f, 0.0f, 0.0f), V(0.0f, 0.0f, 0.0f));
+}
+
+/* detectCollision, :28-123 (types 0 sphere, 1 capsule, 2 box, 3 plane) */
+int zo_detect_collision(const ZoCollider* a, const ZoCollider* b, ZoContactResult* out) {
+    memset(out, 0, sizeof *out);
+    v3 pa = np_point(a, ld3(a->local_pos));
+    v3 pb = np_point(b, ld3(b->local_pos));
+    const uint32_t ta = a->type, tb = b->type;
+    int hit = 0;
+    if (ta == 0) {
+        if (tb == 0) hit = np_sphere_sphere(pa, a->size[0], pb, b->size[0], out);
+        else if (tb == 1) hit = np_sphere_capsule(pa, a->size[0], pb, b, out);
+        else if (tb == 2) hit = np_sphere_box(pa, a->size[0], b, out);
+        else if (tb == 3) hit = np_sphere_plane(pa, a->size[0], b, out);
+    } else if (ta == 1) {
+        if (tb == 0) { hit = np_sphere_capsule(pb, b->size[0], pa, a, out); if (hit) np_flip(out); }
+        else if (tb == 1) hit = np_capsule_capsule(pa, a, pb, b, out);
+        else if (tb == 3) hit = np_capsule_plane(pa, a, b, out);
+    } else if (ta == 2) {
+        if (tb == 0) { hit = np_sphere_box(pb, b->size[0], a, out); if (hit) np_flip(out); }
+        else if (tb == 3) hit = np_box_plane(a, b, out);
+        else if (tb == 2) hit = np_box_box(pa, a, pb, b, out);
+    } else if (ta == 3) {
+        if (tb == 0) { hit = np_sphere_plane(pb, b->size[0], a, out); if (hit) np_flip(out); }
+        else if (tb == 1) { hit = np_capsule_plane(pb, b, a, out); if (hit) np_flip(out); }
+        else if (tb == 2) { hit = np_box_plane(b, a, out); if (hit) np_flip(out); }
+    }
+    if (!hit) memset(out, 0, sizeof *out);
+    return hit;
+}
+
+/* detectCollision over n pairs (the CPU baseline of the batched kernel); OpenMP over pairs. */
+void zo_detect_collisions(const ZoCollider* a, const ZoCollider* b, uint32_t n, ZoContactResult* out, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t i = 0; i < (int64_t)n; ++i) zo_detect_collision(&a[i], &b[i], &out[i]);
+    (void)nthreads;
+}

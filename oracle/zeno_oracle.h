@@ -37,6 +37,27 @@ typedef struct { uint32_t type_object[4]; float params[4]; } ZoSensor;
 typedef struct { uint32_t indices[4]; float anchor_a[4], anchor_b[4], axis_target[4], limits[4], state[4]; } ZoConstraint;
 typedef struct { float position_pen[4], normal_friction[4]; uint32_t indices[4]; float impulses[4]; } ZoContact;
 
+/* One side of a pair for the extended narrow phase (narrow_phase.detectCollision,
+ * src/collision/narrow_phase.zig:28-123): the geom's type, size and local position
+ * (primitives.Geom) and its body's transform (body.Transform). 64 bytes. */
+typedef struct {
+    uint32_t type;         /* GeomType: 0 sphere, 1 capsule, 2 box, 3 plane; others: no contact */
+    float size[3];         /* radius; radius, half length; half extents; plane offset */
+    float local_pos[4];    /* w unused */
+    float position[4];     /* w unused */
+    float quaternion[4];   /* xyzw */
+} ZoCollider;
+
+/* narrow_phase.ContactResult (:12-25). All zero when there is no contact. 64 bytes. */
+typedef struct {
+    float point[3];
+    float penetration;
+    float normal[3];
+    uint32_t valid;
+    float local_a[4];      /* w 0 */
+    float local_b[4];      /* w 0 */
+} ZoContactResult;
+
 /* Per-world constants: SimParams (world.zig:35-56) plus the uploaded scene records. */
 typedef struct {
     uint32_t num_envs, num_bodies, num_joints, num_geoms, num_actuators, num_sensors, obs_dim;
@@ -107,6 +128,11 @@ void zo_collide_env(const ZoModel* m, const float* positions, const float* quate
  * *count in the sequential order described in zeno_oracle.c. */
 void zo_broad_phase_hash(const ZoModel* m, const float* positions, uint32_t* cell_ids,
                          ZoContact* contacts, uint32_t* count);
+
+/* narrow_phase.detectCollision for one pair: 1 and *out filled on contact, else 0. */
+int zo_detect_collision(const ZoCollider* a, const ZoCollider* b, ZoContactResult* out);
+/* The same over n pairs; nthreads <= 0 uses the OpenMP default. */
+void zo_detect_collisions(const ZoCollider* a, const ZoCollider* b, uint32_t n, ZoContactResult* out, int nthreads);
 
 /* match_cached_contacts (all_shaders.metal:1483-1544) on one env, exposed for unit tests. */
 void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,

@@ -142,3 +142,16 @@ def test_model_create_host_only(lib):
     assert (v.num_bodies, v.num_geoms) == (2, 1)
     lib.zeno_amd_model_destroy(h)
     assert not lib.zeno_amd_model_create(b"/nonexistent/model.xml")
+
+
+def test_collision_abi_struct_layouts_and_null_arguments(lib):
+    """ZenoAmdCollider / ZenoAmdContactResult are 64 B records; the oracle's records share
+    the layout; null operands are rejected before any GPU work, and n = 0 is a no-op."""
+    from oracle import oracle as O
+    from zeno_amd import collision as Z
+
+    assert Z.COLLIDER_DTYPE == O.COLLIDER_DTYPE and Z.CONTACT_RESULT_DTYPE == O.CONTACT_RESULT_DTYPE
+    assert Z.COLLIDER_DTYPE.fields["quaternion"][1] == 48 and Z.CONTACT_RESULT_DTYPE.fields["valid"][1] == 28
+    assert lib.zeno_amd_detect_collisions(None, None, 4, None, None) == -6
+    assert lib.zeno_amd_detect_collisions_host(None, None, 4, None) == -6
+    assert lib.zeno_amd_detect_collisions(None, None, 0, None, None) == 0

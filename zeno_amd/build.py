@@ -65,12 +65,12 @@ def build_library() -> Path:
     for src in ("mjcf.cpp", "model.cpp"):
         obj = BUILD / (src + ".o")
         jobs.append([cxx, *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
-    for src in ("step.hip", "world.hip", "capi.hip"):
+    for src in ("step.hip", "world.hip", "capi.hip", "collide.hip"):
         obj = BUILD / (src + ".o")
         jobs.append([hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 4)) as ex:
         list(ex.map(_run, jobs))
-    objs = [str(BUILD / (s + ".o")) for s in ("mjcf.cpp", "model.cpp", "step.hip", "world.hip", "capi.hip")]
+    objs = [str(BUILD / (s + ".o")) for s in ("mjcf.cpp", "model.cpp", "step.hip", "world.hip", "capi.hip", "collide.hip")]
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])
     os.replace(tmp, LIB)

@@ -9,6 +9,7 @@
 
 #include "../../include/zeno.h"
 #include "../../include/zeno_amd_ext.h"
+#include "collide.h"
 #include "world.h"
 
 using za::World;
@@ -437,6 +438,33 @@ int zeno_amd_world_get_cell_ids(ZenoWorldHandle world, uint32_t* out) {
     if (e == hipSuccess) e = hipMemcpyAsync(out, w->d_cell_ids, (size_t)w->E * w->model.num_geoms * 4, hipMemcpyDeviceToHost, w->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(w->stream);
     return hip_status(e, "get_cell_ids");
+}
+
+int zeno_amd_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n, ZenoAmdContactResult* out,
+                               void* stream) {
+    if (n == 0) return ZENO_SUCCESS;
+    if (!a || !b || !out) return ZENO_INVALID_ARGUMENT;
+    return hip_status(za::launch_detect_collisions(a, b, n, out, (hipStream_t)stream), "detect_collisions");
+}
+
+int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                    ZenoAmdContactResult* out) {
+    if (n == 0) return ZENO_SUCCESS;
+    if (!a || !b || !out) return ZENO_INVALID_ARGUMENT;
+    const size_t in_bytes = (size_t)n * sizeof(ZenoAmdCollider), out_bytes = (size_t)n * sizeof(ZenoAmdContactResult);
+    void *da = nullptr, *db = nullptr, *dout = nullptr;
+    hipError_t e = hipMalloc(&da, in_bytes);
+    if (e == hipSuccess) e = hipMalloc(&db, in_bytes);
+    if (e == hipSuccess) e = hipMalloc(&dout, out_bytes);
+    if (e == hipSuccess) e = hipMemcpy(da, a, in_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, b, in_bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = za::launch_detect_collisions((const ZenoAmdCollider*)da, (const ZenoAmdCollider*)db, n,
+                                                          (ZenoAmdContactResult*)dout, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(out, dout, out_bytes, hipMemcpyDeviceToHost);
+    if (da) hipFree(da);
+    if (db) hipFree(db);
+    if (dout) hipFree(dout);
+    return hip_status(e, "detect_collisions_host");
 }
 
 }  // extern "C"

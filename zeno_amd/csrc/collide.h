@@ -1,0 +1,14 @@
+// Batched extended narrow phase (narrow_phase.detectCollision) on the GPU.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/zeno_amd_ext.h"
+
+namespace za {
+
+// One lane per pair: out[i] = detectCollision(a[i], b[i]) for i < n; device pointers.
+hipError_t launch_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n, ZenoAmdContactResult* out,
+                                    hipStream_t stream);
+
+}  // namespace za
