@@ -24,15 +24,16 @@ struct EnvLds {
     uint32_t order;                                                    // u16[M] level of each valid slot
     // Contact schedule, aliased onto arrays that are dead by then: vlist and lst (u16[M]
     // each: valid slots, valid slots by level) share skey; loff (u16[M + 2], level ranges
-    // in lst) shares ppen.
+    // in lst) and the level computation's per-slot dynamic bodies and predecessors
+    // (u32[M] each, at byte 8M and 12M) share ppen.
     uint32_t vlist, lst, loff;
     // Spatial-hash broad phase (scenes above kHashMinGeoms geoms), on skey as well: hkey
     // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom).
     uint32_t hkey, hcell;
+    uint32_t bmask;  // contact levels: u64[B][ceil(M/64)] slot masks per body
     // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
     // when the model blob is read in place from HBM.
     uint32_t jrec;
-    uint32_t last;                                                     // u16[B]
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
     uint32_t bytes;                                                    // total, multiple of 16
 };
@@ -62,8 +63,12 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
     L.hkey = L.skey; L.hcell = L.skey + 4 * (G > kHashMinGeoms ? hash_pad(G) : 0);
+    // Per-body bit masks of the valid contact slots touching the body (u64[B][ceil(M/64)]),
+    // on the force and torque arrays (dead from integration to the next substep) when they fit.
+    const uint32_t mask_words = (M + 63) / 64;
+    L.bmask = 8 * mask_words <= 32 ? L.frc : 0u;
     L.jrec = take(jrec_bytes);
-    L.last = take(2 * B);
+    if (8 * mask_words > 32) L.bmask = take(8 * mask_words * B);
     L.misc = take(16);
     L.bytes = o;
     return L;

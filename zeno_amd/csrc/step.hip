@@ -40,8 +40,9 @@ struct Lds {
     uint32_t* skey;
     float4 *ppen, *pimp;  // prev snapshot: position_pen; impulses.xyz with the pair key in .w
     float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
-    uint16_t *order, *vlist, *lst, *loff, *last;
+    uint16_t *order, *vlist, *lst, *loff;
     uint32_t *hkey, *hcell;  // spatial hash, aliased on skey
+    unsigned long long* bmask;  // contact levels: per-body slot masks
     float4* jrec;            // per-environment solve records (model records in HBM)
     uint32_t* misc;
 };
@@ -64,8 +65,8 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.vlist = (uint16_t*)(base + L.vlist);
     s.lst = (uint16_t*)(base + L.lst);
     s.loff = (uint16_t*)(base + L.loff);
-    s.last = (uint16_t*)(base + L.last);
     s.hkey = (uint32_t*)(base + L.hkey);
+    s.bmask = (unsigned long long*)(base + L.bmask);
     s.hcell = (uint32_t*)(base + L.hcell);
     s.jrec = (float4*)(base + L.jrec);
     s.misc = (uint32_t*)(base + L.misc);
@@ -907,8 +908,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         __syncthreads();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
         // The snapshot is key-sorted (it is a sorted list from the last substep), so the
-        // entries with this slot's body pair form one run found by binary search; scanning
-        // that run in index order gives the reference's first strict minimum.
+        // entries with this slot's body pair form one run whose ends are found by binary
+        // search; scanning that run in index order gives the reference's first strict
+        // minimum.
         if (live) {
             const uint32_t pn = pcount < M ? pcount : M;
             for (uint32_t k = sl; k < n_live; k += G) {
@@ -920,10 +922,16 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     uint32_t mid = (lo + hi) >> 1;
                     if (__float_as_uint(s.pimp[mid].w) < key) lo = mid + 1; else hi = mid;
                 }
+                uint32_t end = lo;
+                hi = pn;
+                while (end < hi) {
+                    uint32_t mid = (end + hi) >> 1;
+                    if (__float_as_uint(s.pimp[mid].w) <= key) end = mid + 1; else hi = mid;
+                }
                 const f3 p = mk3(c->position_pen[0], c->position_pen[1], c->position_pen[2]);
                 float best = 0.04f;
                 int best_i = -1;
-                for (uint32_t i = lo; i < pn && __float_as_uint(s.pimp[i].w) == key; ++i) {
+                for (uint32_t i = lo; i < end; ++i) {
                     const float4 q = s.ppen[i];
                     if (q.w < 0) continue;
                     f3 d = sub(mk3(q.x, q.y, q.z), p);
@@ -942,13 +950,24 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // level(slot) = 1 + max level of earlier valid slots sharing a body that the solve
         // writes (inv_m > 1e-8). Running levels in order reproduces the sequential slot
         // order exactly. Valid slots (solve_contacts skips only pen < 0, :1667) are
-        // compacted in slot order with a ballot; one lane per env then assigns levels and
-        // counting-sorts the slots by level into s.lst, level l owning
-        // [s.loff[l - 1], s.loff[l]).
+        // compacted in slot order with a ballot, and each dynamic body gets a bit mask of
+        // the compacted slots touching it. Along one body the levels increase, so a slot's
+        // level is 1 + the larger level of its predecessors on its two bodies (the highest
+        // lower bit of each body's mask); levels follow by relaxation, one pass per level,
+        // and each level's slots are placed in slot order by a ballot into s.lst, level l
+        // owning [s.loff[l - 1], s.loff[l]).
+        __syncthreads();  // matching has read the snapshot, which the level arrays reuse
         uint32_t nv = 0;
+        const uint32_t mw = (M + 63u) >> 6;                                        // mask words per body
+        uint32_t* const vbod = (uint32_t*)((unsigned char*)s.ppen + 8u * M);    // u32[M] dynamic bodies
+        uint32_t* const prv = (uint32_t*)((unsigned char*)s.ppen + 12u * M);    // u32[M] predecessors
+        const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
+        const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
         if (live) {
-            const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
-            const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
+            for (uint32_t i = sl; i < B * mw; i += G) s.bmask[i] = 0ull;
+        }
+        wave_sync<HBM>();
+        if (live) {
             for (uint32_t base = 0; base < n_live; base += G) {
                 const uint32_t k = base + sl;
                 bool valid = false;
@@ -958,44 +977,81 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     valid = !(s.con[phys].position_pen[3] < 0);
                 }
                 const uint64_t ballot = __ballot(valid);
-                if (valid) s.vlist[nv + (uint32_t)__popcll(ballot & below)] = (uint16_t)phys;
+                if (valid) {
+                    const uint32_t at = nv + (uint32_t)__popcll(ballot & below);
+                    const ContactRec* c = &s.con[phys];
+                    const uint32_t ia = c->indices[0], ib = c->indices[1];
+                    const uint32_t A = (md.flags[ia] & 2u) ? ia : 0xFFFFu, Bd = (md.flags[ib] & 2u) ? ib : 0xFFFFu;
+                    s.vlist[at] = (uint16_t)phys;
+                    vbod[at] = A | (Bd << 16);
+                    const unsigned long long bit = 1ull << (at & 63u);
+                    if (A != 0xFFFFu) atomicOr(&s.bmask[A * mw + (at >> 6)], bit);
+                    if (Bd != 0xFFFFu) atomicOr(&s.bmask[Bd * mw + (at >> 6)], bit);
+                }
                 nv += (uint32_t)__popcll(ballot & group_mask);
             }
-            for (uint32_t b = sl; b < B; b += G) s.last[b] = 0;
         }
-        __syncthreads();
-        if (live && sl == 0) {
+        wave_sync<HBM>();
+        // Predecessor on a body: the highest set bit below slot i in the body's mask.
+        auto pred = [&](uint32_t body, uint32_t i) -> uint32_t {
+            if (body == 0xFFFFu) return 0xFFFFu;
+            for (int w = (int)(i >> 6); w >= 0; --w) {
+                unsigned long long m = s.bmask[body * mw + (uint32_t)w];
+                if ((uint32_t)w == (i >> 6)) m &= (1ull << (i & 63u)) - 1ull;
+                if (m) return (uint32_t)w * 64u + 63u - (uint32_t)__clzll(m);
+            }
+            return 0xFFFFu;
+        };
+        if (live) {
+            for (uint32_t i = sl; i < nv; i += G) {
+                const uint32_t bo = vbod[i];
+                prv[i] = pred(bo & 0xFFFFu, i) | (pred(bo >> 16, i) << 16);
+                s.order[i] = 1;
+            }
+        }
+        wave_sync<HBM>();
+        for (;;) {
+            bool changed = false;
+            if (live) {
+                for (uint32_t i = sl; i < nv; i += G) {
+                    const uint32_t pr = prv[i], pa = pr & 0xFFFFu, pb = pr >> 16;
+                    const uint32_t la = pa != 0xFFFFu ? s.order[pa] : 0u;
+                    const uint32_t lb = pb != 0xFFFFu ? s.order[pb] : 0u;
+                    const uint32_t lv = (la > lb ? la : lb) + 1u;
+                    if (lv != s.order[i]) { s.order[i] = (uint16_t)lv; changed = true; }
+                }
+            }
+            wave_sync<HBM>();
+            if (__ballot(changed) == 0ull) break;
+        }
+        {
             uint32_t nlev = 0;
-            for (uint32_t i = 0; i < nv; ++i) {
-                const ContactRec* c = &s.con[s.vlist[i]];
-                const uint32_t ia = c->indices[0], ib = c->indices[1];
-                const bool da = (md.flags[ia] & 2u) != 0, db = (md.flags[ib] & 2u) != 0;
-                const uint32_t la = da ? s.last[ia] : 0u;
-                const uint32_t lb = db ? s.last[ib] : 0u;
-                const uint32_t lv = (la > lb ? la : lb) + 1;
-                if (da) s.last[ia] = (uint16_t)lv;
-                if (db) s.last[ib] = (uint16_t)lv;
-                s.order[i] = (uint16_t)lv;
-                nlev = lv > nlev ? lv : nlev;
+            if (live) {
+                for (uint32_t i = sl; i < nv; i += G) nlev = s.order[i] > nlev ? s.order[i] : nlev;
             }
-            // Counting sort: loff[l] = count, then the start of level l; placing the slots
-            // in slot order advances loff[l] to the end of level l, so level l ends up
-            // owning [loff[l - 1], loff[l]) with loff[0] = 0.
-            for (uint32_t l = 0; l <= nlev; ++l) s.loff[l] = 0;
-            for (uint32_t i = 0; i < nv; ++i) s.loff[s.order[i]] += 1;
+            for (uint32_t d = 1; d < (uint32_t)G; d <<= 1) {
+                const uint32_t t = __shfl_xor(nlev, d, G);
+                nlev = t > nlev ? t : nlev;
+            }
+            uint32_t wave_nlev = nlev;  // the loop below runs to the largest count of the wave
+            for (uint32_t d = G; d < 64u; d <<= 1) {
+                const uint32_t t = __shfl_xor(wave_nlev, d);
+                wave_nlev = t > wave_nlev ? t : wave_nlev;
+            }
             uint32_t run = 0;
-            for (uint32_t l = 1; l <= nlev; ++l) {
-                const uint32_t c = s.loff[l];
-                s.loff[l] = (uint16_t)run;
-                run += c;
+            if (live && sl == 0) s.loff[0] = 0;
+            for (uint32_t l = 1; l <= wave_nlev; ++l) {
+                for (uint32_t base = 0; base < M; base += G) {
+                    if (__ballot(live && base < nv) == 0ull) break;
+                    const uint32_t i = base + sl;
+                    const bool at_l = live && i < nv && s.order[i] == l;
+                    const uint64_t ballot = __ballot(at_l);
+                    if (at_l) s.lst[run + (uint32_t)__popcll(ballot & below)] = s.vlist[i];
+                    run += (uint32_t)__popcll(ballot & group_mask);
+                }
+                if (live && sl == 0 && l <= nlev) s.loff[l] = (uint16_t)run;
             }
-            for (uint32_t i = 0; i < nv; ++i) {
-                const uint32_t lv = s.order[i];
-                const uint32_t at = s.loff[lv];
-                s.loff[lv] = (uint16_t)(at + 1);
-                s.lst[at] = s.vlist[i];
-            }
-            s.misc[2] = nlev;
+            if (live && sl == 0) s.misc[2] = nlev;
         }
         // Per-slot constants of the contact solve (the same in every iteration): the bias
         // velocity, the two position-correction shares and the summed inverse mass, kept in
