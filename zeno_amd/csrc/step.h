@@ -82,24 +82,30 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
 // order inside the colour, and every phase takes one branch for the whole wave.
 // Templates that the solver skips (types without a solver, or two static bodies) are
 // dropped here.
-constexpr uint32_t kJRecQuads = 7;  // float4 per solve record
+constexpr uint32_t kJRecQuads = 8;  // float4 per solve record
+constexpr uint32_t kJHalfQuads = 4;  // float4 per lane-pair half record
 struct JointPhase { uint32_t type, start, count, pad; };
 
-// Record layout (float4 quads):
-//   q0 = (ia, ib, template index, flags)  [u32]; flags: bit0 inv_m_a > 0, bit1 inv_m_b > 0,
-//        bit2 / bit3 the centre of mass of body a / b is exactly +0
-//   q1 = inverse mass and inertia of body a, q2 = of body b
-//   q3.w = compliance (replaced by compliance / dt^2 in LDS at kernel start)
-//   POSITIONAL: q3.xyz anchor_a, q4.xyz anchor_b, q5.xyz com_a, q6.xyz com_b
+// Record layout (float4 quads). q0 = (ia, ib, template index, flags) [u32]; flags: bit0
+// inv_m_a > 0, bit1 inv_m_b > 0, bit2 / bit3 the centre of mass of body a / b is exactly
+// +0, bits 8-15 the constraint type.
+// Lane-pair types (POSITIONAL, ANGULAR, ANGULAR_LIMIT) hold two halves, quads 0-3 for the
+// lane of body a and quads 4-7 for the lane of body b, each laid out as
+//   h0 = q0,  h1 = inverse mass and inertia of the lane's body,
+//   h2 = (vector, compliance): POSITIONAL the lane's anchor, ANGULAR the lane's axis,
+//        ANGULAR_LIMIT the limit axis; .w is replaced by compliance / dt^2 at kernel start,
+//   h3 = POSITIONAL the lane's centre of mass, ANGULAR_LIMIT (lower, upper), else 0,
+// so each lane reads only its own half and needs no selects between the two bodies.
+// Single-lane types (run by body a's lane) use quads 0-6:
+//   q1 / q2 = inverse mass and inertia of body a / b, q3.w = compliance (-> / dt^2),
 //   WELD:       q3.xyz anchor_a, q4.xyz anchor_b, q5 target quaternion
-//   ANGULAR:    q3.xyz axis_a, q4.xyz axis_b
-//   ANG. LIMIT: q3.xyz axis, q4.xy (lower, upper)
 //   LIN. LIMIT: q3.xyz axis, q4.xyz anchor_b, q5.xy (lower, upper)
 //   SLIDER:     q3.xyz anchor_a, q4.xyz anchor_b, q5.xyz axis, q6 target quaternion
 inline bool joint_type_solved(uint32_t t) {
     return t == C_POSITIONAL || t == C_ANGULAR || t == C_ANGULAR_LIMIT || t == C_LINEAR_LIMIT || t == C_WELD ||
            t == C_SLIDER;
 }
+__host__ __device__ inline bool joint_type_paired(uint32_t t) { return t == C_POSITIONAL || t == C_ANGULAR || t == C_ANGULAR_LIMIT; }
 
 inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const std::vector<uint32_t>& ranges,
                                 const float* invmi /* [B][4] */, const float* com /* [B][4] */,
@@ -128,38 +134,50 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
                     return (b[0] | b[1] | b[2]) == 0u;
                 };
                 const uint32_t flags = (ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u) |
-                                       (pos_zero(com + 4 * ia) ? 4u : 0u) | (pos_zero(com + 4 * ib) ? 8u : 0u);
-                q[0] = make_float4(u(ia), u(ib), u(k), u(flags));
-                q[1] = make_float4(ma[0], ma[1], ma[2], ma[3]);
-                q[2] = make_float4(mb[0], mb[1], mb[2], mb[3]);
+                                       (pos_zero(com + 4 * ia) ? 4u : 0u) | (pos_zero(com + 4 * ib) ? 8u : 0u) |
+                                       (type << 8);
+                const float4 head = make_float4(u(ia), u(ib), u(k), u(flags));
+                const float4 mia = make_float4(ma[0], ma[1], ma[2], ma[3]);
+                const float4 mib = make_float4(mb[0], mb[1], mb[2], mb[3]);
                 const float* A = t.anchor_a;
                 const float* Bv = t.anchor_b;
-                q[3] = make_float4(A[0], A[1], A[2], A[3]);
-                switch (type) {
-                    case C_POSITIONAL:
-                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
-                        q[5] = make_float4(com[4 * ia], com[4 * ia + 1], com[4 * ia + 2], 0);
-                        q[6] = make_float4(com[4 * ib], com[4 * ib + 1], com[4 * ib + 2], 0);
-                        break;
-                    case C_WELD:
-                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
-                        q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], t.axis_target[3]);
-                        break;
-                    case C_ANGULAR:
-                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
-                        break;
-                    case C_ANGULAR_LIMIT:
-                        q[4] = make_float4(t.limits[0], t.limits[1], 0, 0);
-                        break;
-                    case C_LINEAR_LIMIT:
-                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
-                        q[5] = make_float4(t.limits[0], t.limits[1], 0, 0);
-                        break;
-                    case C_SLIDER:
-                        q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
-                        q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], 0);
-                        q[6] = make_float4(t.limits[0], t.limits[1], t.limits[2], t.limits[3]);
-                        break;
+                const float comp = A[3];
+                if (joint_type_paired(type)) {
+                    q[0] = head; q[1] = mia;
+                    q[4] = head; q[5] = mib;
+                    q[2] = make_float4(A[0], A[1], A[2], comp);
+                    switch (type) {
+                        case C_POSITIONAL:
+                            q[6] = make_float4(Bv[0], Bv[1], Bv[2], comp);
+                            q[3] = make_float4(com[4 * ia], com[4 * ia + 1], com[4 * ia + 2], 0);
+                            q[7] = make_float4(com[4 * ib], com[4 * ib + 1], com[4 * ib + 2], 0);
+                            break;
+                        case C_ANGULAR:
+                            q[6] = make_float4(Bv[0], Bv[1], Bv[2], comp);
+                            break;
+                        case C_ANGULAR_LIMIT:
+                            q[6] = q[2];
+                            q[3] = q[7] = make_float4(t.limits[0], t.limits[1], 0, 0);
+                            break;
+                    }
+                } else {
+                    q[0] = head; q[1] = mia; q[2] = mib;
+                    q[3] = make_float4(A[0], A[1], A[2], comp);
+                    switch (type) {
+                        case C_WELD:
+                            q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                            q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], t.axis_target[3]);
+                            break;
+                        case C_LINEAR_LIMIT:
+                            q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                            q[5] = make_float4(t.limits[0], t.limits[1], 0, 0);
+                            break;
+                        case C_SLIDER:
+                            q[4] = make_float4(Bv[0], Bv[1], Bv[2], 0);
+                            q[5] = make_float4(t.axis_target[0], t.axis_target[1], t.axis_target[2], 0);
+                            q[6] = make_float4(t.limits[0], t.limits[1], t.limits[2], t.limits[3]);
+                            break;
+                    }
                 }
                 recs.insert(recs.end(), q, q + kJRecQuads);
                 ++ph.count;

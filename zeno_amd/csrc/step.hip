@@ -148,21 +148,23 @@ __device__ __forceinline__ q4 sel(bool c, q4 x, q4 y) { return c ? x : y; }
 __device__ __forceinline__ f3 signed3(float sg, f3 v) { return {sg * v.x, sg * v.y, sg * v.z}; }
 __device__ __forceinline__ q4 signed4(float sg, q4 v) { return {sg * v.x, sg * v.y, sg * v.z, sg * v.w}; }
 
+// The lane's half of a lane-pair solve record (build_joint_program): header, the lane's
+// body's inverse mass and inertia, its vector (anchor or axis) with compliance / dt^2 in .w,
+// and its centre of mass or the angular limits.
+struct JHalf { float4 h0, mi, v1, v2; };
+__device__ __forceinline__ JHalf load_half(const float4* p) { return JHalf{p[0], p[1], p[2], p[3]}; }
+
 // :934-1037 positional (point-to-point), lane pair.
-__device__ __forceinline__ void solve_positional2(const float4* r, const Lds& s, bool odd) {
-    const float4 q0 = r[0];
-    const uint32_t ia = fbits(q0.x), ib = fbits(q0.y), ci = fbits(q0.z);
+__device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, bool odd) {
+    const uint32_t ia = fbits(h.h0.x), ib = fbits(h.h0.y), ci = fbits(h.h0.z);
     const uint32_t me = odd ? ib : ia;
-    const float4 mi = odd ? r[2] : r[1];
-    const float4 anc = odd ? r[4] : r[3];
-    const float4 com = odd ? r[6] : r[5];
-    const float alpha_tilde = r[3].w;
-    const float inv_mass = mi.x;
-    const f3 iI = mk3(mi.y, mi.z, mi.w);
+    const float alpha_tilde = h.v1.w;
+    const float inv_mass = h.mi.x;
+    const f3 iI = mk3(h.mi.y, h.mi.z, h.mi.w);
     const float sg = odd ? -1.0f : 1.0f;
     const f3 P = xyz(s.pos[me]);
     const q4 Q = toq(s.quat[me]);
-    const f3 rr = qrot(xyz(anc), Q);                       // r_a or r_b
+    const f3 rr = qrot(xyz(h.v1), Q);                      // r_a or r_b
     const f3 u = add(P, rr);                               // pos + r
     const f3 uo = pair_swap(u);
     const f3 diff = sub(sel(odd, uo, u), sel(odd, u, uo));  // (pos_a + r_a) - (pos_b + r_b)
@@ -178,10 +180,10 @@ __device__ __forceinline__ void solve_positional2(const float4* r, const Lds& s,
         const f3 impulse = sscale(d_lambda, n);
         // r - qrot(com, q): with com = +0 and a finite q the rotated offset is exactly +0 and
         // r - (+0) = r, so the rotation is skipped.
-        const bool com_zero = ((fbits(q0.w) >> (odd ? 3 : 2)) & 1u) != 0 && __builtin_isfinite(Q.x) &&
+        const bool com_zero = ((fbits(h.h0.w) >> (odd ? 3 : 2)) & 1u) != 0 && __builtin_isfinite(Q.x) &&
                               __builtin_isfinite(Q.y) && __builtin_isfinite(Q.z) && __builtin_isfinite(Q.w);
         f3 rc = rr;
-        if (!com_zero) rc = sub(rr, qrot(xyz(com), Q));
+        if (!com_zero) rc = sub(rr, qrot(xyz(h.v2), Q));
         if (inv_mass > 0) {
             set_xyz(&s.pos[me], add(P, signed3(sg, scale(impulse, inv_mass))));
             s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(cross(rc, impulse), iI), Q)))));
@@ -190,16 +192,13 @@ __device__ __forceinline__ void solve_positional2(const float4* r, const Lds& s,
 }
 
 // :1131-1186 hinge axis alignment, lane pair.
-__device__ __forceinline__ void solve_angular2(const float4* r, const Lds& s, bool odd) {
-    const float4 q0 = r[0];
-    const uint32_t me = odd ? fbits(q0.y) : fbits(q0.x);
-    const float4 mi = odd ? r[2] : r[1];
-    const float4 ax = odd ? r[4] : r[3];
-    const float alpha_tilde = r[3].w;
-    const float inv_mass = mi.x;
-    const f3 iI = mk3(mi.y, mi.z, mi.w);
+__device__ __forceinline__ void solve_angular2(const JHalf& h, const Lds& s, bool odd) {
+    const uint32_t me = odd ? fbits(h.h0.y) : fbits(h.h0.x);
+    const float alpha_tilde = h.v1.w;
+    const float inv_mass = h.mi.x;
+    const f3 iI = mk3(h.mi.y, h.mi.z, h.mi.w);
     const q4 Q = toq(s.quat[me]);
-    const f3 axw = qrot(xyz(ax), Q);
+    const f3 axw = qrot(xyz(h.v1), Q);
     const f3 axo = pair_swap(axw);
     const f3 cr = cross(sel(odd, axo, axw), sel(odd, axw, axo));
     const float sin_angle = len(cr);
@@ -217,16 +216,14 @@ __device__ __forceinline__ void solve_angular2(const float4* r, const Lds& s, bo
 }
 
 // :1189-1238 angular limit, lane pair.
-__device__ __forceinline__ void solve_angular_limit2(const float4* r, const Lds& s, bool odd) {
-    const float4 q0 = r[0], a3 = r[3], lim = r[4];
-    const uint32_t me = odd ? fbits(q0.y) : fbits(q0.x);
-    const float4 mi = odd ? r[2] : r[1];
-    const float alpha_tilde = a3.w;
-    const float inv_mass = mi.x;
-    const f3 iI = mk3(mi.y, mi.z, mi.w);
+__device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const Lds& s, bool odd) {
+    const uint32_t me = odd ? fbits(h.h0.y) : fbits(h.h0.x);
+    const float alpha_tilde = h.v1.w;
+    const float inv_mass = h.mi.x;
+    const f3 iI = mk3(h.mi.y, h.mi.z, h.mi.w);
     const float sg = odd ? -1.0f : 1.0f;
-    const f3 axis_local = xyz(a3);
-    const float lower = lim.x, upper = lim.y;
+    const f3 axis_local = xyz(h.v1);
+    const float lower = h.v2.x, upper = h.v2.y;
     const q4 Q = toq(s.quat[me]);
     const q4 Qo = pair_swap(Q);
     const q4 qa = sel(odd, Qo, Q), qb = sel(odd, Q, Qo);
@@ -512,6 +509,20 @@ __device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, Cont
     }
 }
 
+// One joint solve of the given type on the lane pair: h is the lane's half record (lane-pair
+// types), r the whole record in LDS (single-lane types, run by body a's lane).
+__device__ __forceinline__ void solve_joint(uint32_t type, const JHalf& h, const float4* r, const Lds& s, bool odd) {
+    switch (type) {
+        case C_POSITIONAL: solve_positional2(h, s, odd); break;
+        case C_ANGULAR: solve_angular2(h, s, odd); break;
+        case C_ANGULAR_LIMIT: solve_angular_limit2(h, s, odd); break;
+        case C_WELD: if (!odd) solve_weld(r, s); break;
+        case C_LINEAR_LIMIT: if (!odd) solve_linear_limit(r, s); break;
+        case C_SLIDER: if (!odd) solve_slider(r, s); break;
+        default: break;
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Spatial-hash broad phase, all_shaders.metal:556-703 (scenes above 512 geoms,
 // world.zig:534). The reference's dense per-env grid (64^3 counters and offsets, a serial
@@ -632,8 +643,13 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
     // this launch: computed once per record.
     for (uint32_t i = tid; i < a.nrec; i += kWave) {
-        float4* q3 = (float4*)md.jrec + i * kJRecQuads + 3;
-        q3->w = q3->w / (a.dt * a.dt);
+        float4* q = (float4*)md.jrec + i * kJRecQuads;
+        if (joint_type_paired((fbits(q[0].w) >> 8) & 0xFFu)) {
+            q[2].w = q[2].w / (a.dt * a.dt);
+            q[6].w = q[6].w / (a.dt * a.dt);
+        } else {
+            q[3].w = q[3].w / (a.dt * a.dt);
+        }
     }
 
     // ---- Load the env's working set (HBM -> LDS) --------------------------------------
@@ -1078,30 +1094,45 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         tick(PH_NARROW);
         // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
         // Phases are same-type runs inside a colour (build_joint_program); the type is
-        // uniform, so each phase takes one scalar branch.
-        for (uint32_t it = 0; it < a.iters; ++it) {
-            for (uint32_t p = 0; p < a.njph; ++p) {
-                const JointPhase ph = md.jph[p];
+        // uniform, so each phase takes one scalar branch. Lane pair (2k, 2k+1) of the env's
+        // lanes takes constraint k. The phase loop is software-pipelined: descriptors and
+        // solve records are read-only, so while phase t runs, the descriptor of phase t + 2
+        // and the lane's first solve record of phase t + 1 are loaded; a phase then starts
+        // with only its bodies' state to read.
+        {
+            const uint32_t nph = a.iters * a.njph;
+            const uint32_t kf = (uint32_t)sl >> 1;
+            const bool odd = (sl & 1) != 0;
+            const uint32_t half = odd ? kJHalfQuads : 0u;
+            JointPhase ph = md.jph[0], ph1 = md.jph[a.njph > 1 ? 1u : 0u];
+            uint32_t p2 = a.njph > 2 ? 2u : 0u;
+            JHalf rec;
+            {
+                const uint32_t st = __builtin_amdgcn_readfirstlane(ph.start), cn = __builtin_amdgcn_readfirstlane(ph.count);
+                rec = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
+            }
+            for (uint32_t t = 0; t < nph; ++t) {
                 const uint32_t type = __builtin_amdgcn_readfirstlane(ph.type);
                 const uint32_t start = __builtin_amdgcn_readfirstlane(ph.start);
                 const uint32_t cnt = __builtin_amdgcn_readfirstlane(ph.count);
+                const JointPhase ph2 = md.jph[p2];
+                JHalf nrec;
+                {
+                    const uint32_t st = __builtin_amdgcn_readfirstlane(ph1.start), cn = __builtin_amdgcn_readfirstlane(ph1.count);
+                    nrec = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
+                }
+                if (live && kf < cnt) solve_joint(type, rec, md.jrec + (start + kf) * kJRecQuads, s, odd);
                 if (live) {
-                    // Lane pair (2k, 2k+1) of the env's lanes takes constraint k.
-                    const bool odd = (sl & 1) != 0;
-                    for (uint32_t k = sl >> 1; k < cnt; k += G / 2) {
+                    for (uint32_t k = kf + G / 2; k < cnt; k += G / 2) {
                         const float4* r = md.jrec + (start + k) * kJRecQuads;
-                        switch (type) {
-                            case C_POSITIONAL: solve_positional2(r, s, odd); break;
-                            case C_ANGULAR: solve_angular2(r, s, odd); break;
-                            case C_ANGULAR_LIMIT: solve_angular_limit2(r, s, odd); break;
-                            case C_WELD: if (!odd) solve_weld(r, s); break;
-                            case C_LINEAR_LIMIT: if (!odd) solve_linear_limit(r, s); break;
-                            case C_SLIDER: if (!odd) solve_slider(r, s); break;
-                            default: break;
-                        }
+                        solve_joint(type, load_half(r + half), r, s, odd);
                     }
                 }
                 wave_sync<HBM>();
+                ph = ph1;
+                ph1 = ph2;
+                p2 = p2 + 1 == a.njph ? 0u : p2 + 1;
+                rec = nrec;
             }
         }
         tick(PH_JOINTS);
