@@ -166,7 +166,9 @@ def bench_collide(n: int, steps: int, warmup: int, cpu_seconds: float, no_cpu: b
         "dtype": "f32", "data": "synthetic: uniform random type pairs, sizes, poses (seed 0)",
         "config": {"workload": f"collide_pairs {n} pairs per launch (operands resident in HBM)", "pairs": n},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None, "kernel": "detect_collisions_kernel",
+                     "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": load_traffic(ROOT / "profiles" / "collide_pairs_hbm_traffic.json") if n == 8388608 else None,
+                     "kernel": "detect_collisions_kernel",
                      "kernel_avg_us": kernel_s * 1e6, "algorithmic_bytes_per_pair": 192,
                      "algorithmic_bytes_per_launch": 192 * n},
     }
@@ -204,12 +206,12 @@ def main() -> int:
     ap.add_argument("--collide-pairs", type=int, default=0,
                     help="instead of the step, time the batched extended narrow phase on this many pairs")
     args = ap.parse_args()
+    if args.calibrate_copy_mib > 0:
+        calibrate_copy(args.calibrate_copy_mib << 20)
     if args.collide_pairs > 0:
         print(json.dumps(bench_collide(args.collide_pairs, min(args.steps, 200), max(args.warmup, 1),
                                        min(args.cpu_seconds, 10.0), args.no_cpu)), flush=True)
         return 0
-    if args.calibrate_copy_mib > 0:
-        calibrate_copy(args.calibrate_copy_mib << 20)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the step shards by environment with no cross-GPU "

@@ -87,7 +87,7 @@ int zeno_amd_world_set_kernel_timing(ZenoWorldHandle world, int enable);
 int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, uint64_t* launches);
 
 /* Launch configuration chosen for the world: environments per wavefront and LDS bytes
- * per workgroup (0 when the working sets live in HBM). */
+ * per workgroup (with the working sets in HBM, the contact and hash arrays kept in LDS). */
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
 
 /* *placement: where the step kernel keeps the scene's model records and each environment's

@@ -40,7 +40,7 @@ def test_placement_parity(name, envs, steps, placement):
     g, o, acts = make_pair(name, envs, steps, seed=9, placement=placement)
     assert g.modes() == {"placement": placement, "spatial_hash": False}
     epw, lds = g.launch_config()
-    assert epw == 1 and (lds == 0) == (placement == 2)
+    assert epw == 1 and lds > 0
     for k in range(steps):
         g.step(acts[k])
         o.step(acts[k])

@@ -28,8 +28,9 @@ struct EnvLds {
     // (u32[M] each, at byte 8M and 12M) share ppen.
     uint32_t vlist, lst, loff;
     // Spatial-hash broad phase (scenes above kHashMinGeoms geoms), on skey as well: hkey
-    // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom).
-    uint32_t hkey, hcell;
+    // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom), hpos/hmeta
+    // (world centre and radius, body / type / masks of each geom).
+    uint32_t hkey, hcell, hpos;
     uint32_t bmask;  // contact levels: u64[B][ceil(M/64)] slot masks per body
     // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
     // when the model blob is read in place from HBM.
@@ -42,6 +43,17 @@ inline uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
 
 // Spatial-hash sort length: G rounded up to a power of two.
 inline uint32_t hash_pad(uint32_t G) { uint32_t p = 1; while (p < G) p <<= 1; return p; }
+// Spatial-hash scratch (on the sort-key region): hkey u32[Gp], hcell u32[G], then 16-B
+// aligned hpos float4[G] (world centre, radius) and hmeta uint4[G] (body, type, contype
+// mask, conaffinity group) of every geom, staged once per substep for the queries.
+inline uint32_t hash_hcell_off(uint32_t G) { return 4 * hash_pad(G); }
+inline uint32_t hash_hpos_off(uint32_t G) { return align16(4 * hash_pad(G) + 4 * G); }
+// staged: with hpos / hmeta (the layout for working sets in HBM, where reading the model
+// records and body poses in the queries would go to global memory).
+inline uint32_t hash_bytes_for(uint32_t G, bool staged) {
+    if (G <= kHashMinGeoms) return 0;
+    return staged ? hash_hpos_off(G) + 32 * G : 4 * (hash_pad(G) + G);
+}
 
 // G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
 // solve records when they are copied per environment (HBM working set), else 0.
@@ -49,7 +61,7 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
-    const uint32_t hash_bytes = G > kHashMinGeoms ? 4 * (hash_pad(G) + G) : 0;
+    const uint32_t hash_bytes = hash_bytes_for(G, false);
     L.pos = take(16 * B); L.quat = take(16 * B); L.vel = take(16 * B); L.angvel = take(16 * B);
     L.ppos = take(16 * B); L.pquat = take(16 * B); L.frc = take(16 * B); L.trq = take(16 * B);
     L.vbefore = take(16 * B);
@@ -62,13 +74,41 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.order = take(2 * M);
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
-    L.hkey = L.skey; L.hcell = L.skey + 4 * (G > kHashMinGeoms ? hash_pad(G) : 0);
+    L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
+    L.hpos = L.skey;  // unused: the queries stage nothing when the working set is in LDS
     // Per-body bit masks of the valid contact slots touching the body (u64[B][ceil(M/64)]),
     // on the force and torque arrays (dead from integration to the next substep) when they fit.
     const uint32_t mask_words = (M + 63) / 64;
     L.bmask = 8 * mask_words <= 32 ? L.frc : 0u;
     L.jrec = take(jrec_bytes);
     if (8 * mask_words > 32) L.bmask = take(8 * mask_words * B);
+    L.misc = take(16);
+    L.bytes = o;
+    return L;
+}
+
+// With the working sets in HBM (placement 2) the arrays that the contact pipeline and the
+// spatial hash touch most (contact records, permutation, sort keys and everything aliased on
+// them, the snapshot, levels, body slot masks) still live in LDS, in this compact layout of
+// their own; only their offsets in the returned EnvLds are meaningful.
+inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0) {
+    EnvLds L{};
+    uint32_t o = 0;
+    auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
+    const uint32_t hash_bytes = hash_bytes_for(G, true);
+    L.con = take(64 * M);
+    L.perm = take(2 * M);
+    const uint32_t mask_bytes = 8 * ((M + 63) / 64) * B;
+    // bmask follows vlist and lst on the sort-key region: the levels run after the sort and
+    // the broad phase are done with it.
+    L.skey = take(std::max(std::max(4 * M + mask_bytes, 16 * Jp), hash_bytes));
+    L.ppen = take(16 * M); L.pimp = take(16 * M);
+    L.order = take(2 * M);
+    L.vlist = L.skey; L.lst = L.skey + 2 * M;
+    L.loff = L.ppen;
+    L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
+    L.hpos = L.skey + (G > kHashMinGeoms ? hash_hpos_off(G) : 0);
+    L.bmask = L.skey + 4 * M;
     L.misc = take(16);
     L.bytes = o;
     return L;
@@ -270,6 +310,7 @@ struct StepArgs {
     uint32_t placement;             // Placement of the model records and working sets
     unsigned char* work;            // PL_ALL_HBM: lds.bytes per environment; else null
     EnvLds lds;
+    EnvLds lds_small;               // PL_ALL_HBM: the arrays kept in LDS (make_env_lds_small)
 };
 
 // Where the step kernel keeps the model records and each environment's working set.

@@ -42,6 +42,8 @@ struct Lds {
     float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
     uint16_t *order, *vlist, *lst, *loff;
     uint32_t *hkey, *hcell;  // spatial hash, aliased on skey
+    float4* hpos;            // spatial hash: geom world centre + radius (then uint4 meta[G])
+    uint32_t *vbod, *prv;    // contact levels: per-slot dynamic bodies and predecessors (on ppen)
     unsigned long long* bmask;  // contact levels: per-body slot masks
     float4* jrec;            // per-environment solve records (model records in HBM)
     uint32_t* misc;
@@ -66,11 +68,39 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.lst = (uint16_t*)(base + L.lst);
     s.loff = (uint16_t*)(base + L.loff);
     s.hkey = (uint32_t*)(base + L.hkey);
+    s.hpos = (float4*)(base + L.hpos);
+    s.vbod = (uint32_t*)(base + L.ppen + 0u);  // placed by bind_levels
+    s.prv = s.vbod;
     s.bmask = (unsigned long long*)(base + L.bmask);
     s.hcell = (uint32_t*)(base + L.hcell);
     s.jrec = (float4*)(base + L.jrec);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
+}
+
+// Rebinds the arrays of make_env_lds_small to base (working sets in HBM, placement 2).
+__device__ __forceinline__ void bind_small(Lds& s, unsigned char* base, const EnvLds& L) {
+    s.con = (ContactRec*)(base + L.con);
+    s.perm = (uint16_t*)(base + L.perm);
+    s.skey = (uint32_t*)(base + L.skey);
+    s.jw = (float4*)(base + L.skey);
+    s.ppen = (float4*)(base + L.ppen); s.pimp = (float4*)(base + L.pimp);
+    s.order = (uint16_t*)(base + L.order);
+    s.vlist = (uint16_t*)(base + L.vlist);
+    s.lst = (uint16_t*)(base + L.lst);
+    s.loff = (uint16_t*)(base + L.loff);
+    s.hkey = (uint32_t*)(base + L.hkey);
+    s.hcell = (uint32_t*)(base + L.hcell);
+    s.hpos = (float4*)(base + L.hpos);
+    s.bmask = (unsigned long long*)(base + L.bmask);
+    s.misc = (uint32_t*)(base + L.misc);
+}
+
+// The level computation's per-slot arrays (u32[M] each) at bytes 8M and 12M of the snapshot
+// position array, which is dead once matching is done.
+__device__ __forceinline__ void bind_levels(Lds& s, uint32_t M) {
+    s.vbod = (uint32_t*)((unsigned char*)s.ppen + 8u * M);
+    s.prv = (uint32_t*)((unsigned char*)s.ppen + 12u * M);
 }
 
 // Model records staged in LDS (see ModelLayout).
@@ -550,12 +580,29 @@ __device__ __forceinline__ uint32_t hash_lower_bound(const uint32_t* key, uint32
 
 // Pairs (g, other > g) of one geom (:632-700). Returns their number; with emit set, writes
 // pair k to logical slot `slot + k` while that is below M.
-__device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t g, bool emit, uint32_t slot) {
-    const GeomRec& ga = md.geoms[g];
-    const uint32_t body_a = ga.type_body[1], type_a = ga.type_body[0];
-    const uint32_t mask_a = ga.type_body[2], group_a = ga.type_body[3];
-    const f3 pa = add(xyz(s.pos[body_a]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
-    const float ra = ga.pos_size0[3];
+// STAGED: the geom data come from hpos / hmeta (working sets in HBM); otherwise from the
+// model records and the body poses directly (both in LDS, or the model records in cache).
+template <bool STAGED>
+__device__ __forceinline__ float4 hash_geom_pos(const Mdl& md, const Lds& s, uint32_t g) {
+    if (STAGED) return s.hpos[g];
+    const GeomRec& gr = md.geoms[g];
+    return tof4(add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2])), gr.pos_size0[3]);
+}
+template <bool STAGED>
+__device__ __forceinline__ uint4 hash_geom_meta(const Mdl& md, const uint4* hmeta, uint32_t g) {
+    if (STAGED) return hmeta[g];
+    const GeomRec& gr = md.geoms[g];
+    return make_uint4(gr.type_body[1], gr.type_body[0], gr.type_body[2], gr.type_body[3]);
+}
+
+template <bool STAGED>
+__device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, uint32_t g, bool emit,
+                                  uint32_t slot) {
+    const float4 pa4 = hash_geom_pos<STAGED>(md, s, g);
+    const uint4 ma = hash_geom_meta<STAGED>(md, hmeta, g);
+    const uint32_t body_a = ma.x, type_a = ma.y, mask_a = ma.z, group_a = ma.w;
+    const f3 pa = xyz(pa4);
+    const float ra = pa4.w;
     const uint32_t id = s.hcell[g];
     const int cx = (int)(id & 63u), cy = (int)((id >> 6) & 63u), cz = (int)(id >> 12);
     const uint32_t xlo = cx > 0 ? (uint32_t)cx - 1u : 0u, xhi = cx < 63 ? (uint32_t)cx + 1u : 63u;
@@ -573,14 +620,14 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
                 if (key > last) break;
                 const uint32_t o = key & 0x3FFFu;
                 if (o <= g) continue;
-                const GeomRec& gb = md.geoms[o];
-                const uint32_t body_b = gb.type_body[1];
+                const uint4 mb = hash_geom_meta<STAGED>(md, hmeta, o);
+                const uint32_t body_b = mb.x;
                 if (body_a == body_b) continue;
-                if ((group_a & gb.type_body[2]) == 0 && (gb.type_body[3] & mask_a) == 0) continue;
-                if (!(type_a == GEOM_PLANE || gb.type_body[0] == GEOM_PLANE)) {
-                    const f3 pb = add(xyz(s.pos[body_b]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
-                    const f3 diff = sub(pb, pa);
-                    const float min_dist = ra + gb.pos_size0[3] + 0.1f;
+                if ((group_a & mb.z) == 0 && (mb.w & mask_a) == 0) continue;
+                if (!(type_a == GEOM_PLANE || mb.y == GEOM_PLANE)) {
+                    const float4 pb4 = hash_geom_pos<STAGED>(md, s, o);
+                    const f3 diff = sub(xyz(pb4), pa);
+                    const float min_dist = ra + pb4.w + 0.1f;
                     if (dot(diff, diff) >= min_dist * min_dist) continue;
                 }
                 if (emit && slot + hits < a.M) {
@@ -614,7 +661,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     const bool live = env < a.E;
     unsigned char* const env_base = HBM ? a.work + (size_t)blockIdx.x * a.lds.bytes
                                         : smem + (PL == PL_LDS ? a.ml.bytes : 0u);
-    const Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
+    Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
+    if (HBM) bind_small(s, smem, a.lds_small);
+    bind_levels(s, a.M);
     Mdl md = bind_model(PL == PL_LDS ? smem : (const unsigned char*)a.model, a.ml);
     if (PL != PL_LDS) md.jrec = s.jrec;
     const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
@@ -792,7 +841,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
         const uint32_t count_before = count;
         if (HASH) {
-            // Cells (broad_phase_count_cells, :556-584) and sort keys; padding keys sort last.
+            uint4* const hmeta = (uint4*)(s.hpos + a.G);
+            // Cells (broad_phase_count_cells, :556-584), sort keys (padding keys sort last)
+            // and each geom's staged centre, radius, body, type and masks.
             if (live) {
                 for (uint32_t g = sl; g < a.Gp; g += G) {
                     uint32_t key = 0xFFFFFFFFu;
@@ -801,6 +852,10 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                         const f3 p = add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2]));
                         const uint32_t id = hash_axis(p.x) + hash_axis(p.y) * 64u + hash_axis(p.z) * 4096u;
                         s.hcell[g] = id;
+                        if (HBM) {
+                            s.hpos[g] = tof4(p, gr.pos_size0[3]);
+                            hmeta[g] = make_uint4(gr.type_body[1], gr.type_body[0], gr.type_body[2], gr.type_body[3]);
+                        }
                         a.cell_ids[(size_t)env * a.G + g] = id;
                         key = (id << 14) | g;
                     }
@@ -827,14 +882,14 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             for (uint32_t base = 0; base < a.G; base += G) {
                 const uint32_t g = base + sl;
                 const bool mine = live && g < a.G;
-                const uint32_t h = mine ? hash_pairs_of(a, md, s, g, false, 0) : 0u;
+                const uint32_t h = mine ? hash_pairs_of<HBM>(a, md, s, hmeta, g, false, 0) : 0u;
                 uint32_t inc = h;
                 for (uint32_t d = 1; d < (uint32_t)G; d <<= 1) {
                     const uint32_t t = __shfl_up(inc, d, G);
                     if ((uint32_t)sl >= d) inc += t;
                 }
                 const uint32_t total = __shfl(inc, G - 1, G);
-                if (mine && h > 0 && count + (inc - h) < M) hash_pairs_of(a, md, s, g, true, count + (inc - h));
+                if (mine && h > 0 && count + (inc - h) < M) hash_pairs_of<HBM>(a, md, s, hmeta, g, true, count + (inc - h));
                 count += total;
             }
         } else {
@@ -975,8 +1030,8 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         __syncthreads();  // matching has read the snapshot, which the level arrays reuse
         uint32_t nv = 0;
         const uint32_t mw = (M + 63u) >> 6;                                        // mask words per body
-        uint32_t* const vbod = (uint32_t*)((unsigned char*)s.ppen + 8u * M);    // u32[M] dynamic bodies
-        uint32_t* const prv = (uint32_t*)((unsigned char*)s.ppen + 12u * M);    // u32[M] predecessors
+        uint32_t* const vbod = s.vbod;  // u32[M] dynamic bodies
+        uint32_t* const prv = s.prv;    // u32[M] predecessors
         const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
         const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
         if (live) {
@@ -1087,7 +1142,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         __syncthreads();
         uint32_t max_lev = 0;
         for (int e2 = 0; e2 < EPW; ++e2) {
-            const uint32_t* m2 = (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
+            const uint32_t* m2 = HBM ? s.misc : (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
             if (blockIdx.x * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
         }
         const uint32_t my_nlev = live ? s.misc[2] : 0u;
@@ -1310,7 +1365,7 @@ int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t
         switch (placement) {
             case PL_LDS: return resident_as<1, PL_LDS, true>(shmem);
             case PL_MODEL_HBM: return hash ? resident_as<1, PL_MODEL_HBM, true>(shmem) : resident_as<1, PL_MODEL_HBM, false>(shmem);
-            case PL_ALL_HBM: return hash ? resident_as<1, PL_ALL_HBM, true>(0) : resident_as<1, PL_ALL_HBM, false>(0);
+            case PL_ALL_HBM: return hash ? resident_as<1, PL_ALL_HBM, true>(shmem) : resident_as<1, PL_ALL_HBM, false>(shmem);
             default: return 0;
         }
     }
@@ -1331,7 +1386,8 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream)
     const size_t env_lds = (size_t)a.lds.bytes * (size_t)envs_per_wave;
     switch (a.placement) {
         case PL_ALL_HBM:
-            return a.hash ? launch_as<1, PL_ALL_HBM, true>(a, blocks, 0, stream) : launch_as<1, PL_ALL_HBM, false>(a, blocks, 0, stream);
+            return a.hash ? launch_as<1, PL_ALL_HBM, true>(a, blocks, a.lds_small.bytes, stream)
+                          : launch_as<1, PL_ALL_HBM, false>(a, blocks, a.lds_small.bytes, stream);
         case PL_MODEL_HBM:
             return a.hash ? launch_as<1, PL_MODEL_HBM, true>(a, blocks, env_lds, stream)
                           : launch_as<1, PL_MODEL_HBM, false>(a, blocks, env_lds, stream);

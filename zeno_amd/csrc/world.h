@@ -30,6 +30,7 @@ struct World {
     int device = 0;
     int epw = 1;
     EnvLds lds{};
+    EnvLds lds_small{};  // placement 2: the arrays kept in LDS
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
     uint32_t placement = PL_LDS;  // where the step kernel keeps model records and working sets
     hipStream_t stream = nullptr;

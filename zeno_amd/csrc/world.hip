@@ -178,6 +178,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
+    const EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms);
     const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec);
     struct Cand { uint32_t pl; int epw; size_t shmem; };
     std::vector<Cand> cands;
@@ -203,7 +204,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
             if (shmem <= lds_max) cands.push_back({PL_LDS, cand, shmem});
         }
         if ((size_t)L_own.bytes <= lds_max) cands.push_back({PL_MODEL_HBM, 1, (size_t)L_own.bytes});
-        cands.push_back({PL_ALL_HBM, 1, 0});
+        cands.push_back({PL_ALL_HBM, 1, (size_t)L_small.bytes});
     }
     const Cand* best = nullptr;
     uint64_t best_score = 0;
@@ -221,6 +222,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     if (best->pl != PL_LDS) L = L_own;
     if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
     w->lds = L;
+    w->lds_small = L_small;
     w->epw = epw;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
@@ -351,6 +353,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.prev_out = d_prev_con;
     a.prev_detached_out = d_prev_detached;
     a.lds = lds;
+    a.lds_small = lds_small;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     const bool timed = timing > 0 && (t_launch++ % (uint64_t)timing) == 0;
     if (timed) {
