@@ -103,6 +103,39 @@ def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
     }
 
 
+# The reference's published step numbers (README.md:56-59,
+# docs/reference/performance.md:13-16): 1024 envs x 1000 steps on an Apple M4 Pro.
+PUBLISHED = {"pendulum": 4.97e6, "cartpole": 6.52e6, "ant": 5.89e6, "humanoid": 5.95e6}
+
+
+def published_configs() -> dict:
+    """The reference's own benchmark (benchmarks/bench_full_physics.zig:37-83) on this build:
+    1024 envs, timestep 0.002, 4 contact iterations, 64 contacts, 1 substep; one action array
+    U[-1, 1] drawn once and reused; 10 warm-up steps, reset, then 1000 zeno_world_step calls
+    on host actions timed by wall clock."""
+    from zeno_amd.scenes import ASSETS
+    from zeno_amd.world import ZenoWorld
+
+    out = {}
+    for name, ref in PUBLISHED.items():
+        w = ZenoWorld(mjcf_path=str(ASSETS / f"{name}.xml"), num_envs=1024, timestep=0.002,
+                      contact_iterations=4, max_contacts_per_env=64, substeps=1)
+        acts = np.random.default_rng(42).uniform(-1.0, 1.0, (1024, max(w.action_dim, 1))).astype(np.float32)
+        acts = acts[:, : w.action_dim]
+        for _ in range(10):
+            w.step(acts)
+        w.reset()
+        w.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(1000):
+            w.step(acts)
+        w.synchronize()
+        v = 1024 * 1000 / (time.perf_counter() - t0)
+        out[name] = {"value": v, "unit": "env-steps/s", "published": ref, "ratio": v / ref}
+        w.close()
+    return out
+
+
 def collide_pairs_inputs(n: int, seed: int = 0):
     """n operand pairs for the extended narrow phase: types uniform over sphere, capsule, box
     and plane on both sides, sizes U[0.05, 0.6], positions U[-0.7, 0.7]^3 (about a third of
@@ -319,6 +352,12 @@ def main() -> int:
         "host_actions": host_loop,
         "finite": finite,
     }
+    if args.workload == "ant" and not args.no_host_loop:
+        result["published_configs"] = {
+            "note": "the reference's own benchmark method and configs (1024 envs, dt 0.002, host actions, "
+                    "1000 steps) on this GPU, beside its published Apple M4 Pro numbers",
+            **published_configs(),
+        }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(model, state, acts, E, args.cpu_seconds)
     print(json.dumps(result), flush=True)
