@@ -77,11 +77,13 @@ def load_traffic(profile_json: Path):
         return None
 
 
-def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
+def cpu_baseline(model, state, acts, num_envs: int, budget_s: float, workload: str = "ant",
+                 max_contacts: int = 64, extended: bool = False) -> dict:
     from oracle.oracle import OracleWorld
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    o = OracleWorld(model, num_envs)
+    o = OracleWorld(model, num_envs, max_contacts_per_env=max_contacts)
+    o.extended_contacts = extended
     o.reset_to_state(*state)
     o.step(acts[0], nthreads=threads)  # warm-up
     # The pregenerated action rows are reused cyclically so that the sample runs for the
@@ -97,7 +99,7 @@ def cpu_baseline(model, state, acts, num_envs: int, budget_s: float) -> dict:
         "unit": "env-steps/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"scalar C oracle (restatement of the reference MSL step), Ant {num_envs} envs x "
+        "sample": f"scalar C oracle (restatement of the reference MSL step), {workload} {num_envs} envs x "
                   f"{steps} steps of the same seeded inputs (action rows reused cyclically), OpenMP over "
                   f"envs, {dt:.1f} s",
     }
@@ -232,6 +234,9 @@ def main() -> int:
     ap.add_argument("--envs", type=int, default=0, help="override the workload's env count")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--max-contacts", type=int, default=64, help="max_contacts_per_env of the world")
+    ap.add_argument("--extended-contacts", action="store_true",
+                    help="extended-contact mode: box and capsule pairs through detectCollision in the step")
     ap.add_argument("--no-host-loop", action="store_true")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run 3 device-to-device copies of this many MiB (a plain copy kernel "
@@ -257,7 +262,9 @@ def main() -> int:
     E = args.envs or wl.num_envs
     total = args.warmup + args.steps
     path, xml, model, state, acts = workload_inputs(args.workload, E, total, seed=0)
-    w = ZenoWorld(mjcf_path=path, mjcf_string=xml, num_envs=E)
+    w = ZenoWorld(mjcf_path=path, mjcf_string=xml, num_envs=E, max_contacts_per_env=args.max_contacts)
+    if args.extended_contacts:
+        w.set_extended_contacts(True)
     epw, lds = w.launch_config()
 
     # Warm-up, then reset to the seeded initial state (bench_full_physics.zig:67-72).
@@ -314,7 +321,9 @@ def main() -> int:
     bytes_env_step = algorithmic_bytes_per_env_step(model, w.max_contacts_per_env)
     bytes_launch = bytes_env_step * E
     achieved = bytes_launch / kernel_avg_s / 1e9
-    prof = ROOT / "profiles" / f"{args.workload}{E}_hbm_traffic.json"
+    tag = f"{args.workload}{E}" + (f"_m{args.max_contacts}" if args.max_contacts != 64 else "") + \
+        ("_ext" if args.extended_contacts else "")
+    prof = ROOT / "profiles" / f"{tag}_hbm_traffic.json"
     traffic = load_traffic(prof)
 
     result = {
@@ -335,6 +344,7 @@ def main() -> int:
             "model": wl.mjcf, "num_envs": E, "timestep": w.timestep, "substeps": 1,
             "contact_iterations": 4, "max_contacts_per_env": w.max_contacts_per_env,
             "envs_per_wave": epw, "lds_bytes_per_workgroup": lds,
+            "extended_contacts": bool(args.extended_contacts), "placement": w.modes()["placement"],
         },
         "hbm_gbps": bytes_env_step * value / 1e9,
         "roofline": {
@@ -359,7 +369,8 @@ def main() -> int:
             **published_configs(),
         }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(model, state, acts, E, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(model, state, acts, E, args.cpu_seconds, args.workload,
+                                              args.max_contacts, args.extended_contacts)
     print(json.dumps(result), flush=True)
     return 0
 

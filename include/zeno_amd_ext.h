@@ -99,6 +99,14 @@ int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave,
  * phase runs (world.zig:534, all_shaders.metal:541-703). Either pointer may be null. */
 int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash);
 
+/* Extended-contact mode, off by default (the reference's step has no such mode). With
+ * enable != 0, the geom pairs that the reference's narrow_phase kernel leaves invalid
+ * (all_shaders.metal:794-893: everything but sphere-sphere, sphere-plane and capsule-plane)
+ * are tested with narrow_phase.detectCollision (narrow_phase.zig:28-123) on the bodies'
+ * poses, so boxes and capsules collide with each other and with spheres; their contacts
+ * enter the contact list and the solve like the others. Takes effect at the next step. */
+int zeno_amd_world_set_extended_contacts(ZenoWorldHandle world, int enable);
+
 /* The spatial hash's cell of every geom in the last substep, [E*G] u32: x + 64 y + 4096 z
  * of the clamped unit-cell coordinates, the reference's cell_ids buffer
  * (world.zig:140,548; all_shaders.metal:576-582), which it keeps without a getter.

@@ -37,7 +37,7 @@ class ZoModel(C.Structure):
         ("timestep", C.c_float), ("gravity", C.c_float * 3),
         ("friction", C.c_float), ("restitution", C.c_float), ("baumgarte", C.c_float), ("slop", C.c_float),
         ("bodies", C.c_void_p), ("joints", C.c_void_p), ("geoms", C.c_void_p), ("actuators", C.c_void_p),
-        ("sensors", C.c_void_p), ("color_ranges", C.c_void_p),
+        ("sensors", C.c_void_p), ("color_ranges", C.c_void_p), ("extended_contacts", C.c_uint32),
     ]
 
 
@@ -136,6 +136,7 @@ class OracleWorld:
         self.prev_contacts = np.zeros((E, M), CONTACT_DTYPE)
         self.prev_contact_counts = np.zeros(E, np.uint32)
         self.cell_ids = np.zeros((E, max(model["num_geoms"], 1)), np.uint32)
+        self.extended_contacts = False
         tmpl = model["constraints"]
         self.constraints = np.ascontiguousarray(np.broadcast_to(tmpl, (E, N)), CONSTRAINT_DTYPE).copy()
         if N:
@@ -163,6 +164,7 @@ class OracleWorld:
         zm.actuators = _p(k["actuators"]) if self.A else None
         zm.sensors = _p(k["sensors"]) if m["num_sensors"] else None
         zm.color_ranges = _p(k["color_ranges"]) if k["color_ranges"].size else None
+        zm.extended_contacts = 1 if self.extended_contacts else 0
         return zm
 
     def _state_struct(self) -> ZoState:

@@ -407,7 +407,7 @@ static void k_sort_contacts(uint32_t M, ZoContact* con, uint32_t raw_count) {
 }
 
 /* narrow_phase, :751-894 */
-static void k_narrow_phase(const ZoModel* m, const float* pos, ZoContact* con, uint32_t raw_count) {
+static void k_narrow_phase(const ZoModel* m, const float* pos, const float* quat, ZoContact* con, uint32_t raw_count) {
     const uint32_t M = m->max_contacts;
     for (uint32_t s = 0; s < M; ++s) {
         if (s >= raw_count) break;
@@ -464,6 +464,30 @@ static void k_narrow_phase(const ZoModel* m, const float* pos, ZoContact* con, u
                 penetration = -dist;
                 contact_point = deepest;
                 contact_point.z = 0;
+                has_contact = 1;
+            }
+        } else if (m->extended_contacts) {
+            /* Extended-contact mode: detectCollision (narrow_phase.zig:28-123) on the geoms
+             * and their bodies' poses; a contact fills the slot as above. solve_contact
+             * moves body a along +normal, so the normal must point from b to a:
+             * detectCollision's does for mixed pairs; capsule-capsule and box-box give a
+             * to b and are negated. */
+            ZoCollider ca, cb;
+            ZoContactResult r;
+            memset(&ca, 0, sizeof ca);
+            memset(&cb, 0, sizeof cb);
+            ca.type = type_a; ca.size[0] = ga->pos_size0[3]; ca.size[1] = ga->params[0]; ca.size[2] = ga->params[1];
+            cb.type = type_b; cb.size[0] = gb->pos_size0[3]; cb.size[1] = gb->params[0]; cb.size[2] = gb->params[1];
+            memcpy(ca.local_pos, ga->pos_size0, 12);
+            memcpy(cb.local_pos, gb->pos_size0, 12);
+            memcpy(ca.position, P4(pos, body_a), 12);
+            memcpy(cb.position, P4(pos, body_b), 12);
+            memcpy(ca.quaternion, P4(quat, body_a), 16);
+            memcpy(cb.quaternion, P4(quat, body_b), 16);
+            if (zo_detect_collision(&ca, &cb, &r)) {
+                normal = type_a == type_b ? vneg(ld3(r.normal)) : ld3(r.normal);
+                penetration = r.penetration;
+                contact_point = ld3(r.point);
                 has_contact = 1;
             }
         }
@@ -943,7 +967,7 @@ static void step_once(Env* e, const float* actions) {
     if (e->m->num_geoms > ZO_HASH_MIN_GEOMS) k_broad_phase_hash(e->m, e->pos, e->cell_ids, e->con, e->count);
     else k_broad_phase(e->m, e->pos, e->B, e->con, e->count);
     k_sort_contacts(e->M, e->con, *e->count);
-    k_narrow_phase(e->m, e->pos, e->con, *e->count);
+    k_narrow_phase(e->m, e->pos, e->quat, e->con, *e->count);
     k_match_cached(e);
     k_solve_joints(e, e->m->contact_iterations);
     k_solve_contacts(e, e->m->contact_iterations);
@@ -1041,7 +1065,6 @@ void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count
 
 void zo_collide_env(const ZoModel* m, const float* positions, const float* quaternions,
                     ZoContact* contacts, uint32_t* count) {
-    (void)quaternions;
     if (m->num_geoms > ZO_HASH_MIN_GEOMS) {
         uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * m->num_geoms);
         k_broad_phase_hash(m, positions, ids, contacts, count);
@@ -1050,7 +1073,7 @@ void zo_collide_env(const ZoModel* m, const float* positions, const float* quate
         k_broad_phase(m, positions, m->num_bodies, contacts, count);
     }
     k_sort_contacts(m->max_contacts, contacts, *count);
-    k_narrow_phase(m, positions, contacts, *count);
+    k_narrow_phase(m, positions, quaternions, contacts, *count);
 }
 
 /* ------------------------------------------------------------------------------------

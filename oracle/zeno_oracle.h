@@ -71,6 +71,9 @@ typedef struct {
     const ZoActuator* actuators;   /* [A] */
     const ZoSensor* sensors;       /* [S] */
     const uint32_t* color_ranges;  /* [num_colors][2] = (offset, count) */
+    /* Extended-contact mode (not in the reference's step): 1 sends the pairs that the
+     * reference's narrow_phase kernel leaves invalid through zo_detect_collision. */
+    uint32_t extended_contacts;
 } ZoModel;
 
 /* Per-env state buffers in the reference layout (state.zig:56-117). J' = max(J,1),

@@ -78,10 +78,10 @@ def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, ato
 
 def make_pair(name: str, num_envs: int, steps: int, seed: int = 0, envs_per_wave: Optional[int] = None,
               substeps: int = 1, max_contacts: int = 64, contact_iterations: int = 4,
-              placement: Optional[int] = None):
+              placement: Optional[int] = None, extended_contacts: bool = False):
     """GPU world and oracle on the same seeded state. envs_per_wave / placement (1: model
     records in HBM, 2: working sets in HBM too) override the launch shape the world would
-    choose."""
+    choose; extended_contacts turns on the extended-contact mode on both."""
     path, xml, model, state, acts = workload_inputs(name, num_envs, steps, seed)
     overrides = {"ZENO_AMD_ENVS_PER_WAVE": None if envs_per_wave is None else str(envs_per_wave),
                  "ZENO_AMD_PLACEMENT": None if placement is None else str(placement)}
@@ -100,6 +100,9 @@ def make_pair(name: str, num_envs: int, steps: int, seed: int = 0, envs_per_wave
                 os.environ[k] = v
     o = OracleWorld(model, num_envs, max_contacts_per_env=max_contacts, substeps=substeps,
                     contact_iterations=contact_iterations)
+    if extended_contacts:
+        g.set_extended_contacts(True)
+        o.extended_contacts = True
     g.reset_to_state(*state)
     o.reset_to_state(*state)
     return g, o, acts

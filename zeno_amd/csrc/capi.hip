@@ -430,6 +430,12 @@ int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_has
     return ZENO_SUCCESS;
 }
 
+int zeno_amd_world_set_extended_contacts(ZenoWorldHandle world, int enable) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    W(world)->ext_contacts = enable != 0;
+    return ZENO_SUCCESS;
+}
+
 int zeno_amd_world_get_cell_ids(ZenoWorldHandle world, uint32_t* out) {
     if (!world) return ZENO_INVALID_HANDLE;
     World* w = W(world);

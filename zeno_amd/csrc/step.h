@@ -281,6 +281,7 @@ struct StepArgs {
     // Sizes. G = geoms; Gp = G rounded up to a power of two (hash mode).
     uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P, G, Gp;
     uint32_t hash;  // 1: spatial-hash broad phase (G > kHashMinGeoms), 0: candidate pair list
+    uint32_t ext_contacts;  // 1: pairs the reference's narrow phase leaves invalid use detectCollision
     uint32_t iters, substeps;
     // Scalars (SimParams, world.zig:35-56).
     float dt, inv_step, gx, gy, gz, restitution, baumgarte, slop;

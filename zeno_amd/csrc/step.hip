@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include "dmath.h"
+#include "narrow_ext.h"
 #include "step.h"
 
 namespace za {
@@ -526,6 +527,25 @@ __device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, Cont
             pen = -dist;
             cp = deepest;
             cp.z = 0;
+            hit = true;
+        }
+    } else if (a.ext_contacts) {
+        // Extended-contact mode (opt-in; the reference's step has none): the pairs its
+        // narrow_phase kernel leaves invalid go through narrow_phase.detectCollision
+        // (narrow_phase.zig:28-123) on the bodies' poses, and a contact becomes a slot
+        // like any other (point, penetration, normal, friction, restitution). The contact
+        // solve pushes body a along +normal, so the slot's normal points from b to a:
+        // detectCollision gives that for every mixed pair and the opposite for
+        // capsule-capsule and box-box, whose normal is negated here.
+        const np::Side sa{type_a, mk3(ga.pos_size0[3], ga.params[0], ga.params[1]),
+                          mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]), xyz(s.pos[body_a]), toq(s.quat[body_a])};
+        const np::Side sb{type_b, mk3(gb.pos_size0[3], gb.params[0], gb.params[1]),
+                          mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]), xyz(s.pos[body_b]), toq(s.quat[body_b])};
+        const np::Result r = np::detect(sa, sb);
+        if (r.valid) {
+            normal = type_a == type_b ? neg(r.normal) : r.normal;
+            pen = r.pen;
+            cp = r.point;
             hit = true;
         }
     }
@@ -1338,9 +1358,15 @@ hipError_t allow_lds(size_t shmem) {
 
 template <int EPW, int PL, bool HASH>
 int resident_as(size_t shmem) {
-    if (allow_lds<EPW, PL, HASH>(shmem) != hipSuccess) return 0;
+    // A shape that does not fit is an answer here, not an error: the failed query's error
+    // is taken off HIP's last-error slot so that later hipGetLastError checks (of this or
+    // another world) do not report it.
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH>, kWave, shmem) != hipSuccess) return 0;
+    if (allow_lds<EPW, PL, HASH>(shmem) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH>, kWave, shmem) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
     return n;
 }
 

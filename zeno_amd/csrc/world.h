@@ -33,6 +33,7 @@ struct World {
     EnvLds lds_small{};  // placement 2: the arrays kept in LDS
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
     uint32_t placement = PL_LDS;  // where the step kernel keeps model records and working sets
+    bool ext_contacts = false;    // extended-contact mode (zeno_amd_world_set_extended_contacts)
     hipStream_t stream = nullptr;
     size_t device_bytes = 0;
 

@@ -216,7 +216,14 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         const uint64_t score = std::min<uint64_t>(w->E, (uint64_t)n * (uint64_t)c.epw * (uint64_t)cus);
         if (!best || score > best_score) { best = &c; best_score = score; }
     }
-    if (!best) { err = "no launch shape fits this scene (ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE?)"; delete w; return nullptr; }
+    if (!best) {
+        err = "no launch shape fits this scene: the smallest per-environment LDS working set is " +
+              std::to_string(L_small.bytes) + " bytes (contacts, sort keys, level masks for max_contacts_per_env=" +
+              std::to_string(w->M) + "), a workgroup may use " + std::to_string(lds_max) +
+              " (or ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE force a shape that cannot launch)";
+        delete w;
+        return nullptr;
+    }
     w->placement = best->pl;
     const int epw = best->epw;
     if (best->pl != PL_LDS) L = L_own;
@@ -332,6 +339,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.nrec = nrec; a.njph = njph; a.M = M; a.P = model.num_pairs;
     a.G = model.num_geoms; a.Gp = hash ? hash_pad(model.num_geoms) : 0; a.hash = hash ? 1u : 0u;
     a.cell_ids = d_cell_ids;
+    a.ext_contacts = ext_contacts ? 1u : 0u;
     a.placement = placement;
     a.work = d_work;
     a.iters = iters; a.substeps = substeps;

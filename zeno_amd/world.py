@@ -385,6 +385,13 @@ class ZenoWorld:
         self._lib.zeno_amd_world_modes(self._handle, C.byref(pl), C.byref(sh))
         return {"placement": pl.value, "spatial_hash": bool(sh.value)}
 
+    def set_extended_contacts(self, enable: bool) -> None:
+        """Extended-contact mode: pairs the reference's narrow phase leaves invalid (box and
+        capsule pairs) are tested with narrow_phase.detectCollision. Off by default."""
+        rc = self._lib.zeno_amd_world_set_extended_contacts(self._handle, 1 if enable else 0)
+        if rc != 0:
+            raise RuntimeError(f"set_extended_contacts failed: {rc}")
+
     def get_cell_ids(self) -> np.ndarray:
         """[num_envs, num_geoms] spatial-hash cell of each geom in the last substep."""
         out = np.zeros((self._num_envs, self.num_geoms), dtype=np.uint32)
