@@ -238,6 +238,7 @@ def main() -> int:
     ap.add_argument("--extended-contacts", action="store_true",
                     help="extended-contact mode: box and capsule pairs through detectCollision in the step")
     ap.add_argument("--no-host-loop", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay leg")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run 3 device-to-device copies of this many MiB (a plain copy kernel "
                          "of known size, used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -298,11 +299,26 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     kernel_ms, launches = w.get_kernel_timing()
     w.set_kernel_timing(False)
+
+    # Third leg (reported beside value): the same K steps captured into one HIP graph
+    # (zeno_amd_world_capture_steps) from the same initial state and replayed with one call.
+    graph_leg = None
+    if not args.no_graph:
+        w.reset_to_state(*state)
+        w.synchronize()
+        w.capture_steps(dptr, stride, args.steps)
+        t2 = time.perf_counter()
+        w.graph_launch()
+        w.synchronize()
+        el3 = time.perf_counter() - t2
+        w.release_graph()
+        graph_leg = {"value": E * args.steps / el3, "ms_per_step": 1e3 * el3 / args.steps,
+                     "method": "the timed steps captured into one HIP graph and replayed with one launch call"}
     dfree()
     value = E * args.steps / elapsed
     kernel_avg_s = (kernel_ms / 1e3) / max(launches, 1)
     pos = w.get_body_positions(zero_copy=False)
-    finite = bool(np.isfinite(pos).all())
+    finite = bool(np.isfinite(pos).all())  # after the graph leg when it ran: same steps, same inputs
 
     # Second leg (reported beside value, never as value): the reference's own method,
     # zeno_world_step with host actions, so the per-step host->device copy is included.
@@ -360,6 +376,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": bytes_launch,
         },
         "host_actions": host_loop,
+        "hip_graph": graph_leg,
         "finite": finite,
     }
     if args.workload == "ant" and not args.no_host_loop:

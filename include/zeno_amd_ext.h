@@ -107,6 +107,21 @@ int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_has
  * enter the contact list and the solve like the others. Takes effect at the next step. */
 int zeno_amd_world_set_extended_contacts(ZenoWorldHandle world, int enable);
 
+/* Captures num_steps consecutive steps into a HIP graph held by the world (replacing an
+ * earlier one); nothing runs until zeno_amd_world_graph_launch. Step k reads its actions
+ * at (const char*)d_actions + k * action_stride_bytes (device memory, E x action_dim f32
+ * each; ignored for scenes without actuators), with substeps as in zeno_world_step. The
+ * graph keeps the kernel arguments of capture time: the setters of timestep, gravity and the
+ * extended-contact mode, and the first zeno_world_step_subset (which allocates its buffers),
+ * release it. No counterpart in the reference (its loop is one zeno_world_step per step);
+ * for callers that replay a fixed device-resident action schedule. */
+int zeno_amd_world_capture_steps(ZenoWorldHandle world, const float* d_actions, uint64_t action_stride_bytes,
+                                 uint32_t num_steps, uint32_t substeps);
+/* Enqueues the captured steps once on the world's stream; returns after enqueueing
+ * (zeno_amd_world_synchronize waits). ZENO_INVALID_ARGUMENT when nothing is captured. */
+int zeno_amd_world_graph_launch(ZenoWorldHandle world);
+int zeno_amd_world_release_graph(ZenoWorldHandle world);
+
 /* The spatial hash's cell of every geom in the last substep, [E*G] u32: x + 64 y + 4096 z
  * of the clamped unit-cell coordinates, the reference's cell_ids buffer
  * (world.zig:140,548; all_shaders.metal:576-582), which it keeps without a getter.

@@ -93,11 +93,14 @@ def test_null_handles(lib):
         assert getattr(lib, f"zeno_world_{count}")(null) == 0, count
     for ext in ["world_get_lambda", "world_get_prev_contact_counts", "world_synchronize",
                 "world_set_kernel_timing", "world_model_view", "world_launch_config", "world_modes",
-                "world_get_cell_ids", "world_set_extended_contacts"]:
+                "world_get_cell_ids", "world_set_extended_contacts", "world_capture_steps",
+                "world_graph_launch", "world_release_graph"]:
         fn = getattr(lib, f"zeno_amd_{ext}")
         args = [None] * len(fn.argtypes)
         if ext in ("world_set_kernel_timing", "world_set_extended_contacts"):
             args[1] = 1
+        if ext == "world_capture_steps":
+            args[2:] = [0, 1, 0]
         assert fn(*args) == -1, ext
     assert lib.zeno_amd_world_step_device(None, None, 0) == -1
     assert lib.zeno_amd_world_get_kernel_timing(None, None, None) == -1

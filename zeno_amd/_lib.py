@@ -164,6 +164,9 @@ SIGNATURES = {
     "zeno_amd_world_modes": (C.c_int, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "zeno_amd_world_get_cell_ids": (C.c_int, [_vp, _u32p]),
     "zeno_amd_world_set_extended_contacts": (C.c_int, [_vp, C.c_int]),
+    "zeno_amd_world_capture_steps": (C.c_int, [_vp, _vp, C.c_uint64, C.c_uint32, C.c_uint32]),
+    "zeno_amd_world_graph_launch": (C.c_int, [_vp]),
+    "zeno_amd_world_release_graph": (C.c_int, [_vp]),
     "zeno_amd_detect_collisions": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "zeno_amd_detect_collisions_host": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
 }

@@ -200,6 +200,7 @@ int zeno_world_set_body_velocities(ZenoWorldHandle world, const float* velocitie
 int zeno_world_set_gravity(ZenoWorldHandle world, float gx, float gy, float gz) {
     if (!world) return ZENO_INVALID_HANDLE;
     World* w = W(world);
+    w->release_graph();
     w->gravity[0] = gx;
     w->gravity[1] = gy;
     w->gravity[2] = gz;
@@ -210,6 +211,7 @@ int zeno_world_set_timestep(ZenoWorldHandle world, float timestep) {
     if (!world) return ZENO_INVALID_HANDLE;
     if (timestep <= 0) return ZENO_INVALID_ARGUMENT;  // NaN passes, as in main.zig:655
     World* w = W(world);
+    w->release_graph();
     w->timestep = timestep;
     w->dt = timestep / (float)(w->cfg_substeps > 1 ? w->cfg_substeps : 1);
     return ZENO_SUCCESS;
@@ -432,7 +434,30 @@ int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_has
 
 int zeno_amd_world_set_extended_contacts(ZenoWorldHandle world, int enable) {
     if (!world) return ZENO_INVALID_HANDLE;
+    W(world)->release_graph();
     W(world)->ext_contacts = enable != 0;
+    return ZENO_SUCCESS;
+}
+
+int zeno_amd_world_capture_steps(ZenoWorldHandle world, const float* d_actions, uint64_t action_stride_bytes,
+                                 uint32_t num_steps, uint32_t substeps) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    World* w = W(world);
+    if (num_steps == 0 || (w->A > 0 && !d_actions)) return ZENO_INVALID_ARGUMENT;
+    if (w->A > 0 && num_steps > 1 && action_stride_bytes < (uint64_t)w->E * w->A * sizeof(float)) return ZENO_INVALID_ARGUMENT;
+    return hip_status(w->capture_steps(d_actions, action_stride_bytes, num_steps, substeps), "capture_steps");
+}
+
+int zeno_amd_world_graph_launch(ZenoWorldHandle world) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    World* w = W(world);
+    if (!w->graph_exec) return ZENO_INVALID_ARGUMENT;
+    return hip_status(w->graph_launch(), "graph_launch");
+}
+
+int zeno_amd_world_release_graph(ZenoWorldHandle world) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    W(world)->release_graph();
     return ZENO_SUCCESS;
 }
 

@@ -87,6 +87,13 @@ struct World {
     std::vector<hipEvent_t> t_events;  // pairs
     size_t t_used = 0;                 // events used (2 per timed launch)
 
+    // A captured multi-step launch sequence (zeno_amd_world_capture_steps). Its kernel
+    // arguments are those of capture time, so the setters that change them release it.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    uint32_t graph_steps = 0;
+    bool capturing = false;
+
     ~World();
     static World* create(const Scene& scene, const ZenoConfig& cfg, std::string& err);
 
@@ -101,6 +108,9 @@ struct World {
     hipError_t get_profiling(ZenoProfilingData* out);
     hipError_t kernel_timing(double* ms, uint64_t* launches);
     uint64_t state_bytes() const;
+    hipError_t capture_steps(const float* d_actions, uint64_t stride_bytes, uint32_t steps, uint32_t substeps);
+    hipError_t graph_launch();
+    void release_graph();
 
    private:
     hipError_t launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask);

@@ -89,6 +89,7 @@ hipError_t fill_u32(hipStream_t s, uint32_t* p, uint32_t n, uint32_t v) {
 
 World::~World() {
     if (stream) hipStreamSynchronize(stream);
+    release_graph();
     void* dev[] = {d_model, d_phase, d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
                    d_jpos, d_jvel, d_jtrq, d_obs, d_lam, d_actions, d_con, d_counts, d_pcounts, d_prev_con,
                    d_prev_detached, d_mask, d_stage, d_cell_ids, d_work};
@@ -363,7 +364,9 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.lds = lds;
     a.lds_small = lds_small;
     hipEvent_t t0 = nullptr, t1 = nullptr;
-    const bool timed = timing > 0 && (t_launch++ % (uint64_t)timing) == 0;
+    // Under capture the launch becomes a graph node; event timing and profiling stay eager-only.
+    const bool timed = !capturing && timing > 0 && (t_launch++ % (uint64_t)timing) == 0;
+    const bool prof_events = profiling && !capturing;
     if (timed) {
         while (t_events.size() < t_used + 2) {
             hipEvent_t ev;
@@ -375,12 +378,12 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
         t_used += 2;
         ZA_TRY(hipEventRecord(t0, stream));
     }
-    if (profiling) {
+    if (prof_events) {
         if (!prof_start) { ZA_TRY(hipEventCreate(&prof_start)); ZA_TRY(hipEventCreate(&prof_stop)); }
         ZA_TRY(hipEventRecord(prof_start, stream));
     }
     ZA_TRY(launch_step(a, epw, stream));
-    if (profiling) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
+    if (prof_events) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
     if (timed) ZA_TRY(hipEventRecord(t1, stream));
     mark_all_dirty();
     return hipSuccess;
@@ -424,8 +427,62 @@ hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_
     return hipSuccess;
 }
 
+void World::release_graph() {
+    // A replay may still be running: the executable graph is destroyed once it is done.
+    if (graph_exec) hipStreamSynchronize(stream);
+    if (graph_exec) hipGraphExecDestroy(graph_exec);
+    if (graph) hipGraphDestroy(graph);
+    graph_exec = nullptr;
+    graph = nullptr;
+    graph_steps = 0;
+}
+
+// `steps` consecutive steps, step k reading its actions at d_actions + k * stride_bytes,
+// captured from the world's stream into one HIP graph: a replay is one launch call for the
+// whole sequence instead of one per step. Every node is a step-kernel launch (no memset or
+// copy nodes). Substeps, dt, gravity, the contact mode and the buffer addresses are fixed at
+// capture; the world's setters for them release the graph.
+hipError_t World::capture_steps(const float* d_act, uint64_t stride_bytes, uint32_t steps, uint32_t substeps) {
+    ZA_TRY(hipSetDevice(device));
+    release_graph();
+    ZA_TRY(hipStreamSynchronize(stream));
+    const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
+    dt = timestep / (float)std::max<uint32_t>(actual, 1);
+    ZA_TRY(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    capturing = true;
+    hipError_t e = hipSuccess;
+    for (uint32_t k = 0; k < steps && e == hipSuccess; ++k) {
+        const float* a = A > 0 ? reinterpret_cast<const float*>(reinterpret_cast<const char*>(d_act) + k * stride_bytes)
+                               : d_actions;
+        e = launch(a, actual, nullptr);
+    }
+    capturing = false;
+    hipGraph_t g = nullptr;
+    const hipError_t ec = hipStreamEndCapture(stream, &g);
+    if (e == hipSuccess) e = ec;
+    if (e == hipSuccess) e = hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        graph_exec = nullptr;
+        (void)hipGetLastError();
+        return e;
+    }
+    graph = g;
+    graph_steps = steps;
+    return hipSuccess;
+}
+
+hipError_t World::graph_launch() {
+    if (!graph_exec) return hipErrorInvalidValue;
+    ZA_TRY(hipSetDevice(device));
+    ZA_TRY(hipGraphLaunch(graph_exec, stream));
+    mark_all_dirty();
+    return hipSuccess;
+}
+
 hipError_t World::ensure_subset_buffers() {
     if (!d_prev_con) {
+        release_graph();  // captured launches hold the buffer addresses of capture time
         ZA_TRY(dalloc(this, &d_prev_con, (size_t)E * std::max<uint32_t>(M, 1)));
         ZA_TRY(dalloc(this, &d_prev_detached, E));
         hipLaunchKernelGGL(fill_u8_kernel, dim3(blocks_for(E, 256)), dim3(256), 0, stream, d_prev_detached, E, (uint8_t)0);

@@ -354,6 +354,29 @@ class ZenoWorld:
             raise RuntimeError(f"get_prev_contact_counts failed: {rc}")
         return out
 
+    def step_device(self, d_actions: int, substeps: int = 0) -> None:
+        """One step with actions already in device memory (address d_actions, E x action_dim
+        f32); returns after enqueueing."""
+        rc = self._lib.zeno_amd_world_step_device(self._handle, C.c_void_p(d_actions or None), substeps)
+        if rc != 0:
+            raise RuntimeError(f"step_device failed: {rc}: {L.last_error()}")
+
+    def capture_steps(self, d_actions: int, stride_bytes: int, num_steps: int, substeps: int = 0) -> None:
+        """Captures num_steps steps into a HIP graph (step k's actions at d_actions + k *
+        stride_bytes in device memory); graph_launch() replays them with one call."""
+        rc = self._lib.zeno_amd_world_capture_steps(self._handle, C.c_void_p(d_actions or None), stride_bytes,
+                                                    num_steps, substeps)
+        if rc != 0:
+            raise RuntimeError(f"capture_steps failed: {rc}: {L.last_error()}")
+
+    def graph_launch(self) -> None:
+        rc = self._lib.zeno_amd_world_graph_launch(self._handle)
+        if rc != 0:
+            raise RuntimeError(f"graph_launch failed: {rc}: {L.last_error()}")
+
+    def release_graph(self) -> None:
+        self._lib.zeno_amd_world_release_graph(self._handle)
+
     def synchronize(self) -> None:
         rc = self._lib.zeno_amd_world_synchronize(self._handle)
         if rc != 0:
