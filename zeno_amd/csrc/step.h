@@ -35,6 +35,9 @@ struct EnvLds {
     // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
     // when the model blob is read in place from HBM.
     uint32_t jrec;
+    // Candidate-pair broad phase with the model records in HBM: each geom's local centre and
+    // radius (float4[G]) and body | type << 16 (u32[G]), staged once per launch.
+    uint32_t gst, gmeta;
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
     uint32_t bytes;                                                    // total, multiple of 16
 };
@@ -57,7 +60,8 @@ inline uint32_t hash_bytes_for(uint32_t G, bool staged) {
 
 // G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
 // solve records when they are copied per environment (HBM working set), else 0.
-inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint32_t G = 0, uint32_t jrec_bytes = 0) {
+inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint32_t G = 0, uint32_t jrec_bytes = 0,
+                           bool stage_geoms = false) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
@@ -82,6 +86,7 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.bmask = 8 * mask_words <= 32 ? L.frc : 0u;
     L.jrec = take(jrec_bytes);
     if (8 * mask_words > 32) L.bmask = take(8 * mask_words * B);
+    if (stage_geoms) { L.gst = take(16 * G); L.gmeta = take(4 * G); }
     L.misc = take(16);
     L.bytes = o;
     return L;
@@ -91,7 +96,7 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
 // spatial hash touch most (contact records, permutation, sort keys and everything aliased on
 // them, the snapshot, levels, body slot masks) still live in LDS, in this compact layout of
 // their own; only their offsets in the returned EnvLds are meaningful.
-inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0) {
+inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0, bool stage_geoms = false) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
@@ -109,6 +114,7 @@ inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G
     L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
     L.hpos = L.skey + (G > kHashMinGeoms ? hash_hpos_off(G) : 0);
     L.bmask = L.skey + 4 * M;
+    if (stage_geoms) { L.gst = take(16 * G); L.gmeta = take(4 * G); }
     L.misc = take(16);
     L.bytes = o;
     return L;

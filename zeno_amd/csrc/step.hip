@@ -47,6 +47,8 @@ struct Lds {
     uint32_t *vbod, *prv;    // contact levels: per-slot dynamic bodies and predecessors (on ppen)
     unsigned long long* bmask;  // contact levels: per-body slot masks
     float4* jrec;            // per-environment solve records (model records in HBM)
+    float4* gst;             // staged geom local centre + radius (model records in HBM, no hash)
+    uint32_t* gmeta;         // staged geom body | type << 16
     uint32_t* misc;
 };
 
@@ -75,6 +77,8 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.bmask = (unsigned long long*)(base + L.bmask);
     s.hcell = (uint32_t*)(base + L.hcell);
     s.jrec = (float4*)(base + L.jrec);
+    s.gst = (float4*)(base + L.gst);
+    s.gmeta = (uint32_t*)(base + L.gmeta);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
 }
@@ -94,6 +98,8 @@ __device__ __forceinline__ void bind_small(Lds& s, unsigned char* base, const En
     s.hcell = (uint32_t*)(base + L.hcell);
     s.hpos = (float4*)(base + L.hpos);
     s.bmask = (unsigned long long*)(base + L.bmask);
+    s.gst = (float4*)(base + L.gst);
+    s.gmeta = (uint32_t*)(base + L.gmeta);
     s.misc = (uint32_t*)(base + L.misc);
 }
 
@@ -195,6 +201,7 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, 
     const float sg = odd ? -1.0f : 1.0f;
     const f3 P = xyz(s.pos[me]);
     const q4 Q = toq(s.quat[me]);
+    const float lambda_prev = s.lam[ci];  // read with the body state: one LDS round trip
     const f3 rr = qrot(xyz(h.v1), Q);                      // r_a or r_b
     const f3 u = add(P, rr);                               // pos + r
     const f3 uo = pair_swap(u);
@@ -205,7 +212,6 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, 
         const f3 rn = cross(rr, n);
         const float t = inv_mass + dot(mul(rn, iI), rn);
         const float w = t + pair_swap(t);                  // (w_a) + (w_b), addition commutes
-        const float lambda_prev = s.lam[ci];
         const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
         if (!odd) s.lam[ci] = lambda_prev + d_lambda;
         const f3 impulse = sscale(d_lambda, n);
@@ -411,14 +417,34 @@ __device__ __forceinline__ void solve_slider(const float4* r, const Lds& s) {
 // solve_contacts on a lane pair: the even lane owns body a, the odd lane body b (see the
 // joint lane pairs). Operands keep the reference's order; body b's updates, which the
 // reference subtracts, are added with a factor of -1.
-__device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md, const Lds& s, uint32_t phys,
-                                               bool odd) {
-    ContactRec* cr = &s.con[phys];
-    const float4 pp = *(const float4*)cr->position_pen;
-    const float4 nf = *(const float4*)cr->normal_friction;
-    const float4 aux = s.pimp[phys];  // (bias, correction share a, share b, inverse mass sum)
-    const uint32_t ia = cr->indices[0], ib = cr->indices[1];
-    const uint32_t me = odd ? ib : ia;
+// The parts of a contact slot the solve reads that do not change during the solve
+// iterations (only impulses.x does, written by the slot's own solve), so they can be read
+// ahead of the slot's turn.
+struct CRec {
+    float4 pp, nf, aux;  // position_pen, normal_friction, (bias, share a, share b, inverse mass sum)
+    uint32_t ia, ib, phys;
+    float rest;          // impulses.w
+};
+
+__device__ __forceinline__ CRec load_crec(const Lds& s, uint32_t phys) {
+    const ContactRec* cr = &s.con[phys];
+    CRec c;
+    c.pp = *(const float4*)cr->position_pen;
+    c.nf = *(const float4*)cr->normal_friction;
+    c.aux = s.pimp[phys];
+    c.ia = cr->indices[0];
+    c.ib = cr->indices[1];
+    c.phys = phys;
+    c.rest = cr->impulses[3];
+    return c;
+}
+
+__device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, const CRec& c, bool odd) {
+    ContactRec* cr = &s.con[c.phys];
+    const float4 pp = c.pp;
+    const float4 nf = c.nf;
+    const float4 aux = c.aux;
+    const uint32_t me = odd ? c.ib : c.ia;
     const float4 imi = md.invmi[me];
     const float inv_mass = imi.x;
     const f3 iI = mk3(imi.y, imi.z, imi.w);
@@ -441,7 +467,7 @@ __device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md,
     const float w_normal = tn + pair_swap(tn);
     if (w_normal < 1e-8f) return;
     const float bias = aux.x;
-    const float restitution = cr->impulses[3];
+    const float restitution = c.rest;
     const float vel_restitution = vel_normal < -0.5f ? restitution * vel_normal : 0.0f;
     float j_n = (-(vel_normal + vel_restitution) + bias) / w_normal;
     j_n = fmaxf(j_n, 0.0f);
@@ -472,6 +498,10 @@ __device__ __forceinline__ void solve_contact2(const StepArgs& a, const Mdl& md,
         set_xyz(&s.angvel[me], w);
     }
     if (!odd) cr->impulses[0] = j_n;
+}
+
+__device__ __forceinline__ void solve_contact2(const Mdl& md, const Lds& s, uint32_t phys, bool odd) {
+    solve_contact_rec(md, s, load_crec(s, phys), odd);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -707,6 +737,13 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     } else {
         const uint4* src = a.model + a.ml.jrec / 16u;
         for (uint32_t i = tid; i < a.nrec * kJRecQuads; i += kWave) ((uint4*)s.jrec)[i] = src[i];
+        if (!HASH) {
+            for (uint32_t g = tid; g < a.G; g += kWave) {
+                const GeomRec& gr = md.geoms[g];
+                s.gst[g] = make_float4(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2], gr.pos_size0[3]);
+                s.gmeta[g] = gr.type_body[1] | (gr.type_body[0] << 16);
+            }
+        }
     }
     __syncthreads();
     // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
@@ -915,25 +952,61 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         } else {
             const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
             const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
+            // With the model records in HBM the geoms come from their LDS copy (s.gst /
+            // s.gmeta) and the loop is software-pipelined over chunks of G pairs: while chunk
+            // k is tested, the pair list of chunk k + 2 (HBM) and the staged geoms of chunk
+            // k + 1 (LDS) are loaded, so a chunk starts with only body positions to read.
+            constexpr bool GSTAGE = PL != PL_LDS;
+            auto pair_at = [&](uint32_t p) -> uint32_t { return (live && p < a.P) ? md.pairs[p] : 0u; };
+            uint32_t pr1 = 0, pr2 = 0, m1a = 0, m1b = 0;
+            float4 c1a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c1b = c1a;
+            if (GSTAGE && a.P > 0) {
+                pr1 = pair_at(sl);
+                pr2 = pair_at(sl + G);
+                m1a = s.gmeta[pr1 & 0xFFFFu]; m1b = s.gmeta[pr1 >> 16];
+                c1a = s.gst[pr1 & 0xFFFFu]; c1b = s.gst[pr1 >> 16];
+            }
             for (uint32_t base = 0; base < a.P; base += G) {
                 const uint32_t p = base + sl;
+                uint32_t pr = 0, m0a = 0, m0b = 0;
+                float4 c0a = c1a, c0b = c1b;
+                if (GSTAGE) {
+                    pr = pr1; m0a = m1a; m0b = m1b;
+                    pr1 = pr2;
+                    pr2 = pair_at(p + 2 * G);
+                    m1a = s.gmeta[pr1 & 0xFFFFu]; m1b = s.gmeta[pr1 >> 16];
+                    c1a = s.gst[pr1 & 0xFFFFu]; c1b = s.gst[pr1 >> 16];
+                }
                 bool hit = false;
                 uint32_t g = 0, h = 0, ba = 0, bb = 0;
                 if (live && p < a.P) {
-                    const uint32_t pr = md.pairs[p];
-                    g = pr & 0xFFFFu;
-                    h = pr >> 16;
-                    const GeomRec& ga = md.geoms[g];
-                    const GeomRec& gb = md.geoms[h];
-                    ba = ga.type_body[1];
-                    bb = gb.type_body[1];
-                    if (ga.type_body[0] == GEOM_PLANE || gb.type_body[0] == GEOM_PLANE) {
+                    float4 ca, cb;
+                    uint32_t ta, tb;
+                    if (GSTAGE) {
+                        g = pr & 0xFFFFu;
+                        h = pr >> 16;
+                        ca = c0a;
+                        cb = c0b;
+                        ba = m0a & 0xFFFFu; ta = m0a >> 16;
+                        bb = m0b & 0xFFFFu; tb = m0b >> 16;
+                    } else {
+                        pr = md.pairs[p];
+                        g = pr & 0xFFFFu;
+                        h = pr >> 16;
+                        const GeomRec& ga = md.geoms[g];
+                        const GeomRec& gb = md.geoms[h];
+                        ba = ga.type_body[1]; ta = ga.type_body[0];
+                        bb = gb.type_body[1]; tb = gb.type_body[0];
+                        ca = *(const float4*)ga.pos_size0;
+                        cb = *(const float4*)gb.pos_size0;
+                    }
+                    if (ta == GEOM_PLANE || tb == GEOM_PLANE) {
                         hit = true;
                     } else {
-                        f3 pa = add(xyz(s.pos[ba]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
-                        f3 pb = add(xyz(s.pos[bb]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
+                        f3 pa = add(xyz(s.pos[ba]), mk3(ca.x, ca.y, ca.z));
+                        f3 pb = add(xyz(s.pos[bb]), mk3(cb.x, cb.y, cb.z));
                         f3 diff = sub(pb, pa);
-                        float min_dist = ga.pos_size0[3] + gb.pos_size0[3] + 0.1f;
+                        float min_dist = ca.w + cb.w + 0.1f;
                         hit = !(dot(diff, diff) >= min_dist * min_dist);  // NaN distances pass, as in :521
                     }
                 }
@@ -1212,16 +1285,44 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         tick(PH_JOINTS);
         // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
-        for (uint32_t it = 0; it < a.iters; ++it) {
-            for (uint32_t lv = 1; lv <= max_lev; ++lv) {
-                if (live && lv <= my_nlev) {
-                    // Lane pair (2j, 2j+1) takes the j-th slot of the level.
-                    const bool odd = (sl & 1) != 0;
-                    const uint32_t end = s.loff[lv];
-                    for (uint32_t j = s.loff[lv - 1] + (sl >> 1); j < end; j += G / 2)
-                        solve_contact2(a, md, s, s.lst[j], odd);
+        // Lane pair (2k, 2k+1) takes the k-th slot of each level (and k + G/2, ... when a
+        // level holds more). The level lists and the slots' static parts are read ahead over
+        // the sequence of (iteration, level) steps: at step f the lane's slot record of step
+        // f + 1, its slot index of step f + 2 and the level bounds of step f + 3 are loaded,
+        // so a step starts with its record in registers and reads only the bodies' state.
+        if (max_lev > 0) {
+            const bool odd = (sl & 1) != 0;
+            const uint32_t kf = (uint32_t)sl >> 1;
+            const uint32_t nsteps = a.iters * max_lev;
+            // Level bounds of step f: slot index j and end of its level; valid when the lane
+            // has a slot there.
+            auto bounds = [&](uint32_t f, uint32_t& j, uint32_t& end) -> bool {
+                const uint32_t lv = f % max_lev + 1u;
+                if (f >= nsteps || !live || lv > my_nlev) { j = end = 0; return false; }
+                j = s.loff[lv - 1] + kf;
+                end = s.loff[lv];
+                return j < end;
+            };
+            uint32_t j0, e0, j1, e1, j2, e2;
+            const bool v0 = bounds(0, j0, e0);
+            bool v1 = bounds(1, j1, e1), v2 = bounds(2, j2, e2);
+            CRec c0 = load_crec(s, v0 ? s.lst[j0] : 0u);
+            bool cv = v0;
+            uint32_t ce = e0, cj = j0;
+            uint32_t p1 = v1 ? s.lst[j1] : 0u;
+            for (uint32_t f = 0; f < nsteps; ++f) {
+                uint32_t j3, e3;
+                const bool v3 = bounds(f + 3, j3, e3);
+                const uint32_t p2 = v2 ? s.lst[j2] : 0u;
+                const CRec c1 = load_crec(s, p1);
+                if (cv) {
+                    solve_contact_rec(md, s, c0, odd);
+                    for (uint32_t j = cj + G / 2; j < ce; j += G / 2) solve_contact2(md, s, s.lst[j], odd);
                 }
                 wave_sync<HBM>();
+                c0 = c1; cv = v1; ce = e1; cj = j1;
+                p1 = p2; v1 = v2; e1 = e2; j1 = j2;
+                v2 = v3; e2 = e3; j2 = j3;
             }
         }
         tick(PH_CONTACTS);

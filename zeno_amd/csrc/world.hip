@@ -179,8 +179,9 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
-    const EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms);
-    const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec);
+    const EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash);
+    const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec,
+                                      !w->hash);
     struct Cand { uint32_t pl; int epw; size_t shmem; };
     std::vector<Cand> cands;
     int force_pl = -1, force_epw = 0;
