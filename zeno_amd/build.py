@@ -7,6 +7,7 @@ Every call recompiles. Objects go to ``zeno_amd/_build/``; the library lands in
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -42,10 +43,32 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libzeno)")
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"build step failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return res.stderr
+
+
+RESOURCES = BUILD / "step_resources.txt"
+
+
+def step_occupancy(remarks: str) -> dict[str, int]:
+    """Waves per SIMD of each step-kernel variant, from the compiler's kernel-resource-usage
+    remarks, keyed "EPW,PL,HASH". The one-environment-per-wave shapes (EPW 1) rely on two
+    resident waves per SIMD to hide memory latency; a change that pushes one of them past
+    256 registers can halve its throughput (the rigid pile's placement-1 kernel: 2.7x)."""
+    occ, name = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: \S*step_kernelILi(\d+)ELi(\d+)ELb(\d)E", line)
+        if m:
+            name = ",".join(m.groups())
+            continue
+        m = re.search(r"Occupancy \[waves/SIMD\]: (\d+)", line)
+        if m and name:
+            occ[name] = int(m.group(1))
+            name = None
+    return occ
 
 
 def build_oracle() -> Path:
@@ -67,9 +90,15 @@ def build_library() -> Path:
         jobs.append([cxx, *CXX_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
     for src in ("step.hip", "world.hip", "capi.hip", "collide.hip"):
         obj = BUILD / (src + ".o")
-        jobs.append([hipcc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        extra = ["-Rpass-analysis=kernel-resource-usage"] if src == "step.hip" else []
+        jobs.append([hipcc, *HIP_FLAGS, *extra, "-c", str(CSRC / src), "-o", str(obj)])
     with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 4)) as ex:
-        list(ex.map(_run, jobs))
+        outs = list(ex.map(_run, jobs))
+    remarks = outs[2]
+    RESOURCES.write_text(remarks)
+    occ = step_occupancy(remarks)
+    print("step_kernel waves per SIMD (EPW,PL,HASH): " + " ".join(f"{k}={v}" for k, v in sorted(occ.items())),
+          file=sys.stderr)
     objs = [str(BUILD / (s + ".o")) for s in ("mjcf.cpp", "model.cpp", "step.hip", "world.hip", "capi.hip", "collide.hip")]
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)])

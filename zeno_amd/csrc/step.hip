@@ -761,6 +761,8 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     // ---- Load the env's working set (HBM -> LDS) --------------------------------------
     uint32_t count = 0, pcount = 0;
     bool detached = false;
+    // The lane's first action (read by stage A of every substep) is loaded with the state.
+    const float act0 = (live && (uint32_t)sl < a.A) ? a.actions[(size_t)env * a.A + sl] : 0.0f;
     if (live) {
         const size_t eb = (size_t)env * B;
         for (uint32_t b = sl; b < B; b += G) {
@@ -774,6 +776,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         for (uint32_t j = sl; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
         for (uint32_t i = sl; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
         const ContactRec* gc = a.contacts + (size_t)env * M;
+#pragma unroll 4
         for (uint32_t k = sl; k < M; k += G) {
             const float4* src = (const float4*)&gc[k];
             float4* dst = (float4*)&s.con[k];
@@ -804,7 +807,8 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
             for (uint32_t k = sl; k < a.A; k += G) {
                 const ActuatorRec& act = md.acts[k];
-                float ctrl = clampf(a.actions[(size_t)env * a.A + k], act.params[1], act.params[2]);
+                const float av = k == (uint32_t)sl ? act0 : a.actions[(size_t)env * a.A + k];
+                float ctrl = clampf(av, act.params[1], act.params[2]);
                 float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
                 s.jt[(uint32_t)act.params[0]] = torque;
             }
