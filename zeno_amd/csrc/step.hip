@@ -1263,17 +1263,19 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 const uint32_t st = __builtin_amdgcn_readfirstlane(ph.start), cn = __builtin_amdgcn_readfirstlane(ph.count);
                 rec = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
             }
-            for (uint32_t t = 0; t < nph; ++t) {
+            // One phase: solves with `cur` (this lane's first record of the phase) while the
+            // next phase's record is loaded into `nxt`. The loop runs two phases per trip with
+            // the two record buffers swapping roles, so no record is copied between phases.
+            auto phase = [&](const JHalf& cur, JHalf& nxt) {
                 const uint32_t type = __builtin_amdgcn_readfirstlane(ph.type);
                 const uint32_t start = __builtin_amdgcn_readfirstlane(ph.start);
                 const uint32_t cnt = __builtin_amdgcn_readfirstlane(ph.count);
                 const JointPhase ph2 = md.jph[p2];
-                JHalf nrec;
                 {
                     const uint32_t st = __builtin_amdgcn_readfirstlane(ph1.start), cn = __builtin_amdgcn_readfirstlane(ph1.count);
-                    nrec = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
+                    nxt = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
                 }
-                if (live && kf < cnt) solve_joint(type, rec, md.jrec + (start + kf) * kJRecQuads, s, odd);
+                if (live && kf < cnt) solve_joint(type, cur, md.jrec + (start + kf) * kJRecQuads, s, odd);
                 if (live) {
                     for (uint32_t k = kf + G / 2; k < cnt; k += G / 2) {
                         const float4* r = md.jrec + (start + k) * kJRecQuads;
@@ -1284,8 +1286,14 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 ph = ph1;
                 ph1 = ph2;
                 p2 = p2 + 1 == a.njph ? 0u : p2 + 1;
-                rec = nrec;
+            };
+            JHalf rec2;
+            uint32_t t = 0;
+            for (; t + 2 <= nph; t += 2) {
+                phase(rec, rec2);
+                phase(rec2, rec);
             }
+            if (t < nph) phase(rec, rec2);
         }
         tick(PH_JOINTS);
         // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
