@@ -1318,24 +1318,32 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             uint32_t j0, e0, j1, e1, j2, e2;
             const bool v0 = bounds(0, j0, e0);
             bool v1 = bounds(1, j1, e1), v2 = bounds(2, j2, e2);
-            CRec c0 = load_crec(s, v0 ? s.lst[j0] : 0u);
+            CRec cA = load_crec(s, v0 ? s.lst[j0] : 0u), cB;
             bool cv = v0;
             uint32_t ce = e0, cj = j0;
             uint32_t p1 = v1 ? s.lst[j1] : 0u;
-            for (uint32_t f = 0; f < nsteps; ++f) {
+            // One step with `cur` while the next step's record is loaded into `nxt`; two
+            // steps per trip with the record buffers swapping roles (no record copies).
+            auto cstep = [&](uint32_t f, const CRec& cur, CRec& nxt) {
                 uint32_t j3, e3;
                 const bool v3 = bounds(f + 3, j3, e3);
                 const uint32_t p2 = v2 ? s.lst[j2] : 0u;
-                const CRec c1 = load_crec(s, p1);
+                nxt = load_crec(s, p1);
                 if (cv) {
-                    solve_contact_rec(md, s, c0, odd);
+                    solve_contact_rec(md, s, cur, odd);
                     for (uint32_t j = cj + G / 2; j < ce; j += G / 2) solve_contact2(md, s, s.lst[j], odd);
                 }
                 wave_sync<HBM>();
-                c0 = c1; cv = v1; ce = e1; cj = j1;
+                cv = v1; ce = e1; cj = j1;
                 p1 = p2; v1 = v2; e1 = e2; j1 = j2;
                 v2 = v3; e2 = e3; j2 = j3;
+            };
+            uint32_t f = 0;
+            for (; f + 2 <= nsteps; f += 2) {
+                cstep(f, cA, cB);
+                cstep(f + 1, cB, cA);
             }
+            if (f < nsteps) cstep(f, cA, cB);
         }
         tick(PH_CONTACTS);
         // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
