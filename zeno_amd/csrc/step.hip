@@ -1306,18 +1306,25 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             const bool odd = (sl & 1) != 0;
             const uint32_t kf = (uint32_t)sl >> 1;
             const uint32_t nsteps = a.iters * max_lev;
-            // Level bounds of step f: slot index j and end of its level; valid when the lane
-            // has a slot there.
-            auto bounds = [&](uint32_t f, uint32_t& j, uint32_t& end) -> bool {
-                const uint32_t lv = f % max_lev + 1u;
-                if (f >= nsteps || !live || lv > my_nlev) { j = end = 0; return false; }
-                j = s.loff[lv - 1] + kf;
+            // Level bounds of step f: the level's first slot index and its end, read raw (the
+            // lane's slot is first + kf); `ok` when the step exists for the lane's env. The
+            // comparison with the end happens a step later, once the read has landed.
+            auto bounds = [&](uint32_t f, uint32_t lv, uint32_t& first, uint32_t& end) -> bool {
+                first = s.loff[lv - 1];
                 end = s.loff[lv];
-                return j < end;
+                return f < nsteps && live && lv <= my_nlev;
             };
+            auto next_lv = [&](uint32_t lv) -> uint32_t { return lv == max_lev ? 1u : lv + 1u; };
             uint32_t j0, e0, j1, e1, j2, e2;
-            const bool v0 = bounds(0, j0, e0);
-            bool v1 = bounds(1, j1, e1), v2 = bounds(2, j2, e2);
+            uint32_t lv3 = 1;
+            bool v0 = bounds(0, lv3, j0, e0);
+            lv3 = next_lv(lv3);
+            bool v1 = bounds(1, lv3, j1, e1);
+            lv3 = next_lv(lv3);
+            bool v2 = bounds(2, lv3, j2, e2);
+            lv3 = next_lv(lv3);
+            j0 += kf; v0 = v0 && j0 < e0;
+            j1 += kf; v1 = v1 && j1 < e1;
             CRec cA = load_crec(s, v0 ? s.lst[j0] : 0u), cB;
             bool cv = v0;
             uint32_t ce = e0, cj = j0;
@@ -1326,7 +1333,10 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             // steps per trip with the record buffers swapping roles (no record copies).
             auto cstep = [&](uint32_t f, const CRec& cur, CRec& nxt) {
                 uint32_t j3, e3;
-                const bool v3 = bounds(f + 3, j3, e3);
+                const bool ok3 = bounds(f + 3, lv3, j3, e3);
+                lv3 = next_lv(lv3);
+                j2 += kf;
+                v2 = v2 && j2 < e2;
                 const uint32_t p2 = v2 ? s.lst[j2] : 0u;
                 nxt = load_crec(s, p1);
                 if (cv) {
@@ -1336,7 +1346,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 wave_sync<HBM>();
                 cv = v1; ce = e1; cj = j1;
                 p1 = p2; v1 = v2; e1 = e2; j1 = j2;
-                v2 = v3; e2 = e3; j2 = j3;
+                v2 = ok3; e2 = e3; j2 = j3;
             };
             uint32_t f = 0;
             for (; f + 2 <= nsteps; f += 2) {
