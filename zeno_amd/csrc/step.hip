@@ -454,9 +454,13 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
     const float friction = nf.w;
     const f3 cp = mk3(pp.x, pp.y, pp.z);
     const float4 P0 = s.pos[me], V0 = s.vel[me], W0 = s.angvel[me];
+    // impulses.x (the slot's normal impulse from the previous iteration, written only by
+    // this solve) is read with the body state, so that read lands in the same round trip.
+    float jn_prev = cr->impulses[0];
     const float sg = odd ? -1.0f : 1.0f;
     const f3 r = sub(cp, xyz(P0));
     const f3 vpt = add(xyz(V0), cross(xyz(W0), r));
+    asm volatile("" : "+v"(jn_prev));
     const f3 vpo = pair_swap(vpt);
     const f3 rel_vel = sub(sel(odd, vpo, vpt), sel(odd, vpt, vpo));
     const float vel_normal = dot(rel_vel, normal);
@@ -478,7 +482,7 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
         w = add(w, signed3(sg, mul(cross(r, impulse_n), iI)));
         set_xyz(&s.pos[me], add(xyz(P0), signed3(sg, sscale(odd ? aux.z : aux.y, normal))));
     }
-    const float j_n_acc = cr->impulses[0] + j_n;
+    const float j_n_acc = jn_prev + j_n;
     if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
         const f3 tangent = divs(vel_tangent, tangent_speed);
         const f3 rt = cross(r, tangent);
