@@ -735,7 +735,10 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
     };
 
-    // ---- Model records (one blob per scene) -> LDS -------------------------------------
+    // ---- Model records (one blob per scene) and the env's working set -> LDS -----------
+    // With the model records in HBM, the working-set reads follow the copy of the solve
+    // records and the geom staging without a barrier in between, so their HBM latencies
+    // overlap.
     if (PL == PL_LDS) {
         for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
     } else {
@@ -749,20 +752,25 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
         }
     }
-    __syncthreads();
+
     // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
-    // this launch: computed once per record.
-    for (uint32_t i = tid; i < a.nrec; i += kWave) {
-        float4* q = (float4*)md.jrec + i * kJRecQuads;
-        if (joint_type_paired((fbits(q[0].w) >> 8) & 0xFFu)) {
-            q[2].w = q[2].w / (a.dt * a.dt);
-            q[6].w = q[6].w / (a.dt * a.dt);
-        } else {
-            q[3].w = q[3].w / (a.dt * a.dt);
+    // this launch: computed once per record, after the records have landed.
+    auto fill_alpha = [&]() {
+        for (uint32_t i = tid; i < a.nrec; i += kWave) {
+            float4* q = (float4*)md.jrec + i * kJRecQuads;
+            if (joint_type_paired((fbits(q[0].w) >> 8) & 0xFFu)) {
+                q[2].w = q[2].w / (a.dt * a.dt);
+                q[6].w = q[6].w / (a.dt * a.dt);
+            } else {
+                q[3].w = q[3].w / (a.dt * a.dt);
+            }
         }
+    };
+    if (PL == PL_LDS) {
+        __syncthreads();
+        fill_alpha();
     }
 
-    // ---- Load the env's working set (HBM -> LDS) --------------------------------------
     uint32_t count = 0, pcount = 0;
     bool detached = false;
     // The lane's first action (read by stage A of every substep) is loaded with the state.
@@ -792,6 +800,7 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
     }
     __syncthreads();
+    if (PL != PL_LDS) fill_alpha();
     tick(PH_LOAD);
 
     for (uint32_t step = 0; step < a.substeps; ++step) {
