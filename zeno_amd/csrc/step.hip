@@ -216,9 +216,11 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, 
         if (!odd) s.lam[ci] = lambda_prev + d_lambda;
         const f3 impulse = sscale(d_lambda, n);
         // r - qrot(com, q): with com = +0 and a finite q the rotated offset is exactly +0 and
-        // r - (+0) = r, so the rotation is skipped.
-        const bool com_zero = ((fbits(h.h0.w) >> (odd ? 3 : 2)) & 1u) != 0 && __builtin_isfinite(Q.x) &&
-                              __builtin_isfinite(Q.y) && __builtin_isfinite(Q.z) && __builtin_isfinite(Q.w);
+        // r - (+0) = r, so the rotation is skipped. A finite sum of the components implies
+        // four finite components (an infinite or NaN one makes the sum infinite or NaN); a
+        // finite q whose sum overflows just takes the rotation.
+        const bool com_zero = ((fbits(h.h0.w) >> (odd ? 3 : 2)) & 1u) != 0 &&
+                              __builtin_isfinite((Q.x + Q.y) + (Q.z + Q.w));
         f3 rc = rr;
         if (!com_zero) rc = sub(rr, qrot(xyz(h.v2), Q));
         if (inv_mass > 0) {
