@@ -63,17 +63,18 @@ struct World {
     float* h_rewards = nullptr;
     uint8_t* h_dones = nullptr;
 
-    // Host actions: a pinned staging ring and a device ring, copied on their own stream so
-    // the copy for the next step overlaps the current step's kernel. act_copied[i] marks
-    // the copy into slot i done (the step waits on it), act_evt[i] the step that read it.
-    static constexpr int kStage = 3;
-    hipStream_t cstream = nullptr;
+    // Host actions: a ring of pinned, coherent host buffers that the step kernel reads in
+    // place over PCIe (with the rest of its input, at the start of the launch), so a step on
+    // host actions needs no separate copy. One event marks the end of every kActGroup
+    // host-action steps; before the first step of a group the host waits for the event of
+    // the group two back, whose steps used the slots this group refills.
+    static constexpr int kStage = 8;
+    static constexpr int kActGroup = kStage / 2;
     float* h_act[kStage] = {};
-    float* d_act_ring = nullptr;  // [kStage][E * A']
-    hipEvent_t act_evt[kStage] = {};
-    hipEvent_t act_copied[kStage] = {};
-    bool act_evt_used[kStage] = {};
-    int act_slot = 0;
+    const float* d_act_view[kStage] = {};  // device addresses of h_act
+    hipEvent_t act_evt[2] = {};
+    bool act_evt_used[2] = {};
+    uint64_t act_steps = 0;  // host-action steps staged and launched
     uint8_t* h_mask_stage = nullptr;
 
     // Profiling and kernel timing.

@@ -97,17 +97,14 @@ World::~World() {
     for (int i = 0; i < MIR_COUNT_ALL; ++i) if (h_mirror[i]) hipHostFree(h_mirror[i]);
     for (int i = 0; i < kStage; ++i) {
         if (h_act[i]) hipHostFree(h_act[i]);
-        if (act_evt[i]) hipEventDestroy(act_evt[i]);
-        if (act_copied[i]) hipEventDestroy(act_copied[i]);
     }
+    for (hipEvent_t ev : act_evt) if (ev) hipEventDestroy(ev);
     if (h_mask_stage) hipHostFree(h_mask_stage);
     std::free(h_rewards);
     std::free(h_dones);
     if (prof_start) hipEventDestroy(prof_start);
     if (prof_stop) hipEventDestroy(prof_stop);
     for (hipEvent_t ev : t_events) hipEventDestroy(ev);
-    if (d_act_ring) hipFree(d_act_ring);
-    if (cstream) hipStreamDestroy(cstream);
     if (stream) hipStreamDestroy(stream);
 }
 
@@ -235,8 +232,6 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->epw = epw;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
-    if ((e = hipStreamCreateWithFlags(&w->cstream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
-    if ((e = dalloc(w, &w->d_act_ring, (size_t)kStage * w->E * w->Ap)) != hipSuccess) return fail("hipMalloc", e);
 
     // Model blob: every per-scene record the kernel reads, packed per ModelLayout.
     w->ml = ML;
@@ -318,10 +313,16 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->h_rewards = (float*)std::calloc(w->E, sizeof(float));
     w->h_dones = (uint8_t*)std::calloc(w->E, 1);
     for (int i = 0; i < kStage; ++i) {
-        if ((e = hipHostMalloc((void**)&w->h_act[i], (size_t)w->E * w->Ap * 4, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
-        if ((e = hipEventCreateWithFlags(&w->act_evt[i], hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
-        if ((e = hipEventCreateWithFlags(&w->act_copied[i], hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
+        // Coherent (fine-grained) so that the kernel reads what the host wrote before the launch
+        // and no stale cached copy of a reused slot.
+        if ((e = hipHostMalloc((void**)&w->h_act[i], (size_t)w->E * w->Ap * 4, hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess)
+            return fail("hipHostMalloc", e);
+        void* dv = nullptr;
+        if ((e = hipHostGetDevicePointer(&dv, w->h_act[i], 0)) != hipSuccess) return fail("hipHostGetDevicePointer", e);
+        w->d_act_view[i] = (const float*)dv;
     }
+    for (hipEvent_t& ev : w->act_evt)
+        if ((e = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
     if ((e = hipHostMalloc((void**)&w->h_mask_stage, w->E, hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
     if ((e = hipStreamSynchronize(w->stream)) != hipSuccess) return fail("init", e);
     return w;
@@ -393,25 +394,26 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
 // World.step, world.zig:694-746: substeps 0 selects the configured count; dt = timestep /
 // substeps; accelerations come from the velocity change over the whole call.
 hipError_t World::stage_actions(const float* actions, const float** d_out, int* slot_out) {
-    const int slot = act_slot;
-    act_slot = (act_slot + 1) % kStage;
-    // The step that last read this slot (and the copy that fed it) must be done before the
-    // pinned and device buffers are reused.
-    if (act_evt_used[slot]) ZA_TRY(hipEventSynchronize(act_evt[slot]));
-    const size_t bytes = (size_t)E * A * sizeof(float);
-    float* d = d_act_ring + (size_t)slot * E * Ap;
-    std::memcpy(h_act[slot], actions, bytes);
-    ZA_TRY(hipMemcpyAsync(d, h_act[slot], bytes, hipMemcpyHostToDevice, cstream));
-    ZA_TRY(hipEventRecord(act_copied[slot], cstream));
-    ZA_TRY(hipStreamWaitEvent(stream, act_copied[slot], 0));
-    *d_out = d;
+    const uint64_t k = act_steps;
+    const int slot = (int)(k % kStage);
+    const int ev = (int)((k / kActGroup) % 2);
+    // The steps that last read this group's slots (the group two back) must be done before
+    // the host refills them.
+    if (k % kActGroup == 0 && act_evt_used[ev]) ZA_TRY(hipEventSynchronize(act_evt[ev]));
+    std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
+    *d_out = d_act_view[slot];
     *slot_out = slot;
     return hipSuccess;
 }
 
 hipError_t World::mark_actions_used(int slot) {
-    ZA_TRY(hipEventRecord(act_evt[slot], stream));
-    act_evt_used[slot] = true;
+    (void)slot;
+    const uint64_t k = act_steps++;
+    if (k % kActGroup == kActGroup - 1) {
+        const int ev = (int)((k / kActGroup) % 2);
+        ZA_TRY(hipEventRecord(act_evt[ev], stream));
+        act_evt_used[ev] = true;
+    }
     return hipSuccess;
 }
 
