@@ -115,8 +115,8 @@ struct World {
 
    private:
     hipError_t launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask);
-    hipError_t stage_actions(const float* actions, const float** d_out, int* slot);
-    hipError_t mark_actions_used(int slot);
+    hipError_t stage_actions(const float* actions, const float** d_out);
+    hipError_t mark_actions_used();
     hipError_t upload_mask(const uint8_t* mask, uint8_t** d_out);
     hipError_t ensure_subset_buffers();
     void mark_all_dirty();

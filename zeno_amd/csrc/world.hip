@@ -393,7 +393,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
 
 // World.step, world.zig:694-746: substeps 0 selects the configured count; dt = timestep /
 // substeps; accelerations come from the velocity change over the whole call.
-hipError_t World::stage_actions(const float* actions, const float** d_out, int* slot_out) {
+hipError_t World::stage_actions(const float* actions, const float** d_out) {
     const uint64_t k = act_steps;
     const int slot = (int)(k % kStage);
     const int ev = (int)((k / kActGroup) % 2);
@@ -402,12 +402,10 @@ hipError_t World::stage_actions(const float* actions, const float** d_out, int* 
     if (k % kActGroup == 0 && act_evt_used[ev]) ZA_TRY(hipEventSynchronize(act_evt[ev]));
     std::memcpy(h_act[slot], actions, (size_t)E * A * sizeof(float));
     *d_out = d_act_view[slot];
-    *slot_out = slot;
     return hipSuccess;
 }
 
-hipError_t World::mark_actions_used(int slot) {
-    (void)slot;
+hipError_t World::mark_actions_used() {
     const uint64_t k = act_steps++;
     if (k % kActGroup == kActGroup - 1) {
         const int ev = (int)((k / kActGroup) % 2);
@@ -422,11 +420,11 @@ hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_
     const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
     dt = timestep / (float)std::max<uint32_t>(actual, 1);
     const float* d_act = d_actions;
-    int slot = -1;
+    bool staged = false;
     if (actions_on_device) d_act = actions;
-    else if (A > 0) ZA_TRY(stage_actions(actions, &d_act, &slot));
+    else if (A > 0) { ZA_TRY(stage_actions(actions, &d_act)); staged = true; }
     ZA_TRY(launch(d_act, actual, nullptr));
-    if (slot >= 0) ZA_TRY(mark_actions_used(slot));
+    if (staged) ZA_TRY(mark_actions_used());
     return hipSuccess;
 }
 
@@ -516,12 +514,12 @@ hipError_t World::step_subset(const float* actions, const uint8_t* mask, uint32_
     const uint32_t actual = substeps == 0 ? adaptive_substeps : substeps;
     dt = timestep / (float)std::max<uint32_t>(actual, 1);
     const float* d_act = d_actions;
-    int slot = -1;
-    if (A > 0) ZA_TRY(stage_actions(actions, &d_act, &slot));
+    bool staged = false;
+    if (A > 0) { ZA_TRY(stage_actions(actions, &d_act)); staged = true; }
     uint8_t* dm = nullptr;
     ZA_TRY(upload_mask(mask, &dm));
     ZA_TRY(launch(d_act, actual, dm));
-    if (slot >= 0) ZA_TRY(mark_actions_used(slot));
+    if (staged) ZA_TRY(mark_actions_used());
     return hipSuccess;
 }
 
