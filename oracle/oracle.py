@@ -7,6 +7,7 @@ scalar restatement of the reference's step, on state arrays in the reference's l
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 from typing import Any, Dict, Optional
 
@@ -53,11 +54,14 @@ _lib = None
 
 
 def load() -> C.CDLL:
+    """The oracle library: oracle/libzeno_oracle.so, or the build named by ZENO_ORACLE_LIB
+    (the sanitizer test loads an ASan/UBSan build of the same source that way)."""
     global _lib
     if _lib is None:
-        if not LIB_PATH.exists():
-            raise RuntimeError(f"oracle library missing: {LIB_PATH} (build with python -m zeno_amd.build)")
-        lib = C.CDLL(str(LIB_PATH))
+        path = Path(os.environ.get("ZENO_ORACLE_LIB", str(LIB_PATH)))
+        if not path.exists():
+            raise RuntimeError(f"oracle library missing: {path} (build with python -m zeno_amd.build)")
+        lib = C.CDLL(str(path))
         lib.zo_step.restype = C.c_int
         lib.zo_step.argtypes = [C.POINTER(ZoModel), C.POINTER(ZoState), C.c_void_p, C.c_uint32,
                                 C.c_uint32, C.c_uint32, C.c_int]
