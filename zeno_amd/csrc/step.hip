@@ -1091,9 +1091,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         __syncthreads();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
         // The snapshot is key-sorted (it is a sorted list from the last substep), so the
-        // entries with this slot's body pair form one run whose ends are found by binary
-        // search; scanning that run in index order gives the reference's first strict
-        // minimum.
+        // entries with this slot's body pair form one run: its first entry is found by binary
+        // search and the run is scanned in index order up to the first other key, which gives
+        // the reference's first strict minimum.
         if (live) {
             const uint32_t pn = pcount < M ? pcount : M;
             for (uint32_t k = sl; k < n_live; k += G) {
@@ -1105,16 +1105,11 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     uint32_t mid = (lo + hi) >> 1;
                     if (__float_as_uint(s.pimp[mid].w) < key) lo = mid + 1; else hi = mid;
                 }
-                uint32_t end = lo;
-                hi = pn;
-                while (end < hi) {
-                    uint32_t mid = (end + hi) >> 1;
-                    if (__float_as_uint(s.pimp[mid].w) <= key) end = mid + 1; else hi = mid;
-                }
                 const f3 p = mk3(c->position_pen[0], c->position_pen[1], c->position_pen[2]);
                 float best = 0.04f;
                 int best_i = -1;
-                for (uint32_t i = lo; i < end; ++i) {
+                // The run ends at the first entry with another key (the list is sorted).
+                for (uint32_t i = lo; i < pn && __float_as_uint(s.pimp[i].w) == key; ++i) {
                     const float4 q = s.ppen[i];
                     if (q.w < 0) continue;
                     f3 d = sub(mk3(q.x, q.y, q.z), p);
