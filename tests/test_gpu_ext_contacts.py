@@ -11,13 +11,19 @@ from tests.parity import compare, gpu_arrays, make_pair, oracle_arrays
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("name,envs,steps,M,placement", [("pile", 8, 12, 512, None),
-                                                         ("pile", 4, 8, 512, 2),
-                                                         ("pile_hash", 4, 6, 512, None),
-                                                         ("ant", 16, 20, 64, None)])
-def test_extended_contacts_parity(name, envs, steps, M, placement):
+# One environment per workgroup with M >= 64 runs the narrow phase grouped by geom-type pair
+# (every placement, with and without the hash, is covered below); Ant at four environments
+# per wave runs it ungrouped.
+@pytest.mark.parametrize("name,envs,steps,M,placement,epw", [("pile", 8, 12, 512, None, None),
+                                                             ("pile", 4, 8, 512, 2, None),
+                                                             ("pile", 4, 8, 512, 0, 1),
+                                                             ("pile_hash", 4, 6, 512, None, None),
+                                                             ("pile_hash", 2, 4, 512, 2, None),
+                                                             ("ant", 16, 20, 128, None, 1),
+                                                             ("ant", 16, 20, 64, None, None)])
+def test_extended_contacts_parity(name, envs, steps, M, placement, epw):
     g, o, acts = make_pair(name, envs, steps, seed=5, max_contacts=M, placement=placement,
-                           extended_contacts=True)
+                           envs_per_wave=epw, extended_contacts=True)
     active = 0
     for k in range(steps):
         g.step(acts[k])

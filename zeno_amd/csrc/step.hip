@@ -702,13 +702,16 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
 // and one working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work).
 // HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms) instead of the
 // candidate pair list. Both non-LDS placements and the hash run one environment per
-// workgroup.
-template <int EPW, int PL, bool HASH>
+// workgroup. GROUP: the narrow phase visits the slots grouped by geom-type pair (the
+// extended-contact mode, one environment per workgroup); a separate instance, so that the
+// other shapes' register allocation is not touched by it.
+template <int EPW, int PL, bool HASH, bool GROUP>
 __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
     constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
+    static_assert(!GROUP || EPW == 1, "type-grouped narrow phase: one environment per workgroup");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int le = tid / G;
@@ -1085,7 +1088,56 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         tick(PH_BROAD);
         // ---- F: narrow_phase (:751-894) -----------------------------------------------
         const uint32_t n_live = count < M ? count : M;
-        if (live) {
+        if (GROUP && a.ext_contacts && M >= 64) {
+            // Extended mode: each slot's pair type picks one of detectCollision's branches,
+            // and a wave runs every branch that its lanes need. The slots are visited grouped
+            // by (type a, type b): a counting sort over the 64 ordered type pairs into s.order
+            // (dead until the levels), with the class counters on s.skey (dead after the
+            // sort). Each slot's result depends on that slot alone, so the visiting order
+            // changes no result.
+            uint32_t* ccount = s.skey;
+            auto geom_type = [&](uint32_t g) -> uint32_t {
+                if (PL != PL_LDS && !HASH) return s.gmeta[g] >> 16;
+                return md.geoms[g].type_body[0];
+            };
+            auto slot_class = [&](uint32_t phys) -> uint32_t {
+                const uint32_t* idx = s.con[phys].indices;
+                return (geom_type(idx[2]) & 7u) * 8u + (geom_type(idx[3]) & 7u);
+            };
+            constexpr uint32_t kPer = 64u / G;  // classes per lane
+            for (uint32_t i = 0; i < kPer; ++i) ccount[sl * kPer + i] = 0u;
+            __syncthreads();
+            if (live) {
+                for (uint32_t k = sl; k < n_live; k += G) atomicAdd(&ccount[slot_class(s.perm[k])], 1u);
+            }
+            __syncthreads();
+            // Exclusive scan of the env's 64 counters: each lane sums its kPer classes, the
+            // env's G lanes scan those sums, and each lane writes its classes' offsets.
+            uint32_t sum = 0;
+            for (uint32_t i = 0; i < kPer; ++i) sum += ccount[sl * kPer + i];
+            uint32_t incl = sum;
+            for (int d = 1; d < G; d <<= 1) {
+                const uint32_t t = __shfl_up(incl, d, G);
+                if (sl >= d) incl += t;
+            }
+            uint32_t run = incl - sum;
+            for (uint32_t i = 0; i < kPer; ++i) {
+                const uint32_t c = ccount[sl * kPer + i];
+                ccount[sl * kPer + i] = run;
+                run += c;
+            }
+            __syncthreads();
+            if (live) {
+                for (uint32_t k = sl; k < n_live; k += G) {
+                    const uint32_t phys = s.perm[k];
+                    s.order[atomicAdd(&ccount[slot_class(phys)], 1u)] = (uint16_t)phys;
+                }
+            }
+            __syncthreads();
+            if (live) {
+                for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.order[k]]);
+            }
+        } else if (live) {
             for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.perm[k]]);
         }
         __syncthreads();
@@ -1487,34 +1539,34 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         if (_e != hipSuccess) return _e; \
     } while (0)
 
-template <int EPW, int PL, bool HASH>
+template <int EPW, int PL, bool HASH, bool GROUP = false>
 hipError_t allow_lds(size_t shmem) {
     // Workgroups above 64 KB of dynamic LDS must opt in per kernel (gfx950 has 160 KB / CU).
     static size_t granted = 64 * 1024;
     if (shmem <= granted) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, PL, HASH>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, PL, HASH, GROUP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e == hipSuccess) granted = shmem;
     return e;
 }
 
-template <int EPW, int PL, bool HASH>
+template <int EPW, int PL, bool HASH, bool GROUP = false>
 int resident_as(size_t shmem) {
     // A shape that does not fit is an answer here, not an error: the failed query's error
     // is taken off HIP's last-error slot so that later hipGetLastError checks (of this or
     // another world) do not report it.
     int n = 0;
-    if (allow_lds<EPW, PL, HASH>(shmem) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH>, kWave, shmem) != hipSuccess) {
+    if (allow_lds<EPW, PL, HASH, GROUP>(shmem) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH, GROUP>, kWave, shmem) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
     return n;
 }
 
-template <int EPW, int PL, bool HASH>
+template <int EPW, int PL, bool HASH, bool GROUP = false>
 hipError_t launch_as(const StepArgs& a, uint32_t blocks, size_t shmem, hipStream_t stream) {
-    ZA_CHECK((allow_lds<EPW, PL, HASH>(shmem)));
-    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH>), dim3(blocks), dim3(kWave), shmem, stream, a);
+    ZA_CHECK((allow_lds<EPW, PL, HASH, GROUP>(shmem)));
+    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH, GROUP>), dim3(blocks), dim3(kWave), shmem, stream, a);
     return hipGetLastError();
 }
 
@@ -1551,6 +1603,23 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream)
     if ((a.placement != PL_LDS || a.hash) && envs_per_wave != 1) return hipErrorInvalidValue;
     if ((a.placement == PL_ALL_HBM) != (a.work != nullptr)) return hipErrorInvalidValue;
     const size_t env_lds = (size_t)a.lds.bytes * (size_t)envs_per_wave;
+    const size_t shmem = (size_t)a.ml.bytes + env_lds;
+    // Extended-contact mode with one environment per workgroup: the instance whose narrow
+    // phase visits the slots grouped by geom-type pair (same results, less divergence).
+    if (a.ext_contacts && a.M >= 64 && envs_per_wave == 1) {
+        switch (a.placement) {
+            case PL_ALL_HBM:
+                return a.hash ? launch_as<1, PL_ALL_HBM, true, true>(a, blocks, a.lds_small.bytes, stream)
+                              : launch_as<1, PL_ALL_HBM, false, true>(a, blocks, a.lds_small.bytes, stream);
+            case PL_MODEL_HBM:
+                return a.hash ? launch_as<1, PL_MODEL_HBM, true, true>(a, blocks, env_lds, stream)
+                              : launch_as<1, PL_MODEL_HBM, false, true>(a, blocks, env_lds, stream);
+            case PL_LDS:
+                return a.hash ? launch_as<1, PL_LDS, true, true>(a, blocks, shmem, stream)
+                              : launch_as<1, PL_LDS, false, true>(a, blocks, shmem, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (a.placement) {
         case PL_ALL_HBM:
             return a.hash ? launch_as<1, PL_ALL_HBM, true>(a, blocks, a.lds_small.bytes, stream)
@@ -1561,7 +1630,6 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream)
         case PL_LDS: break;
         default: return hipErrorInvalidValue;
     }
-    const size_t shmem = (size_t)a.ml.bytes + env_lds;
     if (a.hash) return launch_as<1, PL_LDS, true>(a, blocks, shmem, stream);
     switch (envs_per_wave) {
         case 1: return launch_as<1, PL_LDS, false>(a, blocks, shmem, stream);
