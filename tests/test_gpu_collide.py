@@ -54,6 +54,20 @@ def test_all_type_pairs_bitwise():
     assert gpu["valid"][(ta >= 4) | (tb >= 4)].sum() == 0
 
 
+def test_shuffled_mixed_batch_bitwise():
+    """Every type pair (heightfield included) in random order, so that each 256-pair block
+    holds most classes and the kernel's in-block grouping by type pair reorders nearly every
+    pair; 20,001 pairs end in a partial block."""
+    rng = np.random.default_rng(7)
+    n = 20001
+    ta, tb = rng.integers(0, 7, n), rng.integers(0, 7, n)
+    a, b = random_colliders(rng, n, ta), random_colliders(rng, n, tb)
+    gpu = Z.detect_collisions(a, b)
+    assert_bitwise(gpu, O.detect_collisions(a, b))
+    assert gpu["valid"].sum() > 1000
+    assert gpu["valid"][(ta >= 4) | (tb >= 4)].sum() == 0
+
+
 def test_degenerate_cases_bitwise():
     cases = []
 

@@ -11,34 +11,96 @@ namespace za {
 namespace {
 using namespace np;
 
-// Each lane loads its own two operand records (consecutive lanes, consecutive 64-B records:
-// the four 16-B loads of a wave cover whole cache lines between them). Results go through
-// LDS so that each store instruction of a wave writes 1 KB of consecutive memory (lane l
-// stores quads l, l + 64, l + 128, l + 192 of the wave's 4 KB block). 16 KB of LDS per
-// 256-lane block leaves occupancy to the register budget.
+// A block takes 256 consecutive pairs. A pair's geom types select one of detect()'s branches
+// and a wave runs every branch its lanes need, so a mixed batch would pay for most of them in
+// every wave. Each lane loads its own pair's two 64-B records (consecutive lanes, consecutive
+// records: one streaming pass), and the block orders its pairs by ordered type pair (64
+// classes), stably: each wave counts its lanes class by class with ballots (one round per
+// class present in the wave), the counts are scanned over (class, wave), and lane t then
+// evaluates the pair at position t of that order. A one-type block keeps every pair in place
+// and evaluates it from registers; a pair that moved is read again from the block's records,
+// which the first pass has just brought into the caches. Each pair's result depends on that
+// pair alone, so the order changes no result. Results go through LDS at the pair's own
+// position, so that each store instruction of a wave writes 1 KB of consecutive memory (lane
+// l stores quads l, l + 64, l + 128, l + 192 of its wave's 4 KB block).
 constexpr int kCollideBlock = 256;
+constexpr int kCollideWaves = kCollideBlock / 64;
 constexpr int kRecQuads = 4;  // 64-B records
+constexpr uint32_t kClasses = 64;
 
 __global__ __launch_bounds__(kCollideBlock) void detect_collisions_kernel(const ZenoAmdCollider* a, const ZenoAmdCollider* b,
                                                                           uint32_t n, ZenoAmdContactResult* out) {
-    __shared__ float4 stage[kCollideBlock / 64][64 * kRecQuads];
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const size_t base = (size_t)blockIdx.x * kCollideBlock + (size_t)wave * 64u;  // first pair of this wave
-    const size_t i = base + lane;
+    __shared__ float4 stage[kCollideBlock * kRecQuads];   // 16 KB: results, pair-major
+    __shared__ uint32_t wcount[kCollideWaves][kClasses];  // lanes of each class per wave, then offsets
+    __shared__ uint16_t order[kCollideBlock];
+    const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
+    const size_t blk = (size_t)blockIdx.x * kCollideBlock;
+    const size_t i = blk + t;
+    wcount[wave][lane] = 0u;
+    float4 q[2 * kRecQuads];
+    uint32_t cls = kClasses - 1u;  // lanes past the end: the last class, evaluated as nothing
+    if (i < n) {
+        const float4* pa = reinterpret_cast<const float4*>(a + i);
+        const float4* pb = reinterpret_cast<const float4*>(b + i);
+#pragma unroll
+        for (int k = 0; k < kRecQuads; ++k) { q[k] = pa[k]; q[kRecQuads + k] = pb[k]; }
+        cls = (__float_as_uint(q[0].x) & 7u) * 8u + (__float_as_uint(q[kRecQuads].x) & 7u);
+    }
+    __syncthreads();
+    uint32_t rank = 0;  // position among the wave's lanes of this class
+    uint64_t pending = __ballot(1);
+    while (pending) {
+        const int leader = __ffsll((unsigned long long)pending) - 1;
+        const uint32_t c = __shfl(cls, leader);
+        const uint64_t same = __ballot(cls == c);
+        if ((int)lane == leader) wcount[wave][c] = (uint32_t)__popcll(same);
+        if (cls == c) rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+        pending &= ~same;
+    }
+    __syncthreads();
+    if (wave == 0) {  // offsets in (class, wave) order: lane c scans class c's total
+        uint32_t cnt[kCollideWaves];
+        uint32_t tot = 0;
+#pragma unroll
+        for (int w = 0; w < kCollideWaves; ++w) { cnt[w] = wcount[w][lane]; tot += cnt[w]; }
+        uint32_t incl = tot;
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t x = __shfl_up(incl, d);
+            if ((int)lane >= d) incl += x;
+        }
+        uint32_t run = incl - tot;
+#pragma unroll
+        for (int w = 0; w < kCollideWaves; ++w) { wcount[w][lane] = run; run += cnt[w]; }
+    }
+    __syncthreads();
+    order[wcount[wave][cls] + rank] = (uint16_t)t;
+    __syncthreads();
+    const uint32_t src = order[t];
+    const size_t j = blk + src;
     Result r = miss();
-    if (i < n) r = detect(load_side(a + i), load_side(b + i));
-    float4* so = stage[wave] + lane * kRecQuads;
+    if (j < n) {
+        if (src != t) {
+            const float4* pa = reinterpret_cast<const float4*>(a + j);
+            const float4* pb = reinterpret_cast<const float4*>(b + j);
+#pragma unroll
+            for (int k = 0; k < kRecQuads; ++k) { q[k] = pa[k]; q[kRecQuads + k] = pb[k]; }
+        }
+        r = detect(side_from(q[0], q[1], q[2], q[3]), side_from(q[4], q[5], q[6], q[7]));
+    }
+    float4* so = stage + src * kRecQuads;
     so[0] = make_float4(r.point.x, r.point.y, r.point.z, r.pen);
     so[1] = make_float4(r.normal.x, r.normal.y, r.normal.z, __uint_as_float(r.valid ? 1u : 0u));
     so[2] = make_float4(r.la.x, r.la.y, r.la.z, 0.0f);
     so[3] = make_float4(r.lb.x, r.lb.y, r.lb.z, 0.0f);
     __syncthreads();
+    const size_t base = blk + (size_t)wave * 64u;  // first pair of this wave's store block
     const size_t nq = (size_t)n * kRecQuads;
     float4* qo = reinterpret_cast<float4*>(out) + base * kRecQuads;
+    const float4* sw = stage + wave * 64u * kRecQuads;
 #pragma unroll
     for (int k = 0; k < kRecQuads; ++k) {
-        const uint32_t q = lane + 64u * k;
-        if (base * kRecQuads + q < nq) qo[q] = stage[wave][q];
+        const uint32_t qq = lane + 64u * k;
+        if (base * kRecQuads + qq < nq) qo[qq] = sw[qq];
     }
 }
 

@@ -27,9 +27,8 @@ struct Side {
     q4 q;
 };
 
-__device__ __forceinline__ Side load_side(const ZenoAmdCollider* c) {
-    const float4* p = reinterpret_cast<const float4*>(c);
-    const float4 r0 = p[0], r1 = p[1], r2 = p[2], r3 = p[3];
+// A ZenoAmdCollider record as its four 16-B quads.
+__device__ __forceinline__ Side side_from(float4 r0, float4 r1, float4 r2, float4 r3) {
     Side s;
     s.type = __float_as_uint(r0.x);
     s.size = mk3(r0.y, r0.z, r0.w);
@@ -37,6 +36,10 @@ __device__ __forceinline__ Side load_side(const ZenoAmdCollider* c) {
     s.pos = mk3(r2.x, r2.y, r2.z);
     s.q = mk4(r3.x, r3.y, r3.z, r3.w);
     return s;
+}
+__device__ __forceinline__ Side load_side(const ZenoAmdCollider* c) {
+    const float4* p = reinterpret_cast<const float4*>(c);
+    return side_from(p[0], p[1], p[2], p[3]);
 }
 
 __device__ __forceinline__ float np_min(float a, float b) { return a != a ? b : (b != b ? a : (a < b ? a : b)); }
