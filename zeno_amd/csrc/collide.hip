@@ -17,12 +17,14 @@ using namespace np;
 // records: one streaming pass), and the block orders its pairs by ordered type pair (64
 // classes), stably: each wave counts its lanes class by class with ballots (one round per
 // class present in the wave), the counts are scanned over (class, wave), and lane t then
-// evaluates the pair at position t of that order. A one-type block keeps every pair in place
-// and evaluates it from registers; a pair that moved is read again from the block's records,
-// which the first pass has just brought into the caches. Each pair's result depends on that
-// pair alone, so the order changes no result. Results go through LDS at the pair's own
-// position, so that each store instruction of a wave writes 1 KB of consecutive memory (lane
-// l stores quads l, l + 64, l + 128, l + 192 of its wave's 4 KB block).
+// evaluates the pair at position t of that order. The records move to their new lanes
+// through one 16 KB LDS buffer, operand a then operand b (column-major: quad k of pair p at
+// k * 256 + p, so the lanes' 16-B accesses of one quad are consecutive). A block of one type
+// pair (every lane's class equal to lane 0's) skips the ordering and the exchange. Every record is read from HBM once. Each
+// pair's result depends on that pair alone, so the order changes no result. Results go
+// through the same buffer at the pair's own position, so that each store instruction of a
+// wave writes 1 KB of consecutive memory (lane l stores quads l, l + 64, l + 128, l + 192 of
+// its wave's 4 KB block).
 constexpr int kCollideBlock = 256;
 constexpr int kCollideWaves = kCollideBlock / 64;
 constexpr int kRecQuads = 4;  // 64-B records
@@ -30,14 +32,17 @@ constexpr uint32_t kClasses = 64;
 
 __global__ __launch_bounds__(kCollideBlock) void detect_collisions_kernel(const ZenoAmdCollider* a, const ZenoAmdCollider* b,
                                                                           uint32_t n, ZenoAmdContactResult* out) {
-    __shared__ float4 stage[kCollideBlock * kRecQuads];   // 16 KB: results, pair-major
+    __shared__ float4 stage[kCollideBlock * kRecQuads];   // 16 KB: operand exchange, then results
     __shared__ uint32_t wcount[kCollideWaves][kClasses];  // lanes of each class per wave, then offsets
     __shared__ uint16_t order[kCollideBlock];
+    __shared__ uint32_t cls0;
     const uint32_t t = threadIdx.x, wave = t >> 6, lane = t & 63u;
     const size_t blk = (size_t)blockIdx.x * kCollideBlock;
     const size_t i = blk + t;
     wcount[wave][lane] = 0u;
     float4 q[2 * kRecQuads];
+#pragma unroll
+    for (int k = 0; k < 2 * kRecQuads; ++k) q[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     uint32_t cls = kClasses - 1u;  // lanes past the end: the last class, evaluated as nothing
     if (i < n) {
         const float4* pa = reinterpret_cast<const float4*>(a + i);
@@ -46,47 +51,51 @@ __global__ __launch_bounds__(kCollideBlock) void detect_collisions_kernel(const 
         for (int k = 0; k < kRecQuads; ++k) { q[k] = pa[k]; q[kRecQuads + k] = pb[k]; }
         cls = (__float_as_uint(q[0].x) & 7u) * 8u + (__float_as_uint(q[kRecQuads].x) & 7u);
     }
+    if (t == 0) cls0 = cls;
     __syncthreads();
-    uint32_t rank = 0;  // position among the wave's lanes of this class
-    uint64_t pending = __ballot(1);
-    while (pending) {
-        const int leader = __ffsll((unsigned long long)pending) - 1;
-        const uint32_t c = __shfl(cls, leader);
-        const uint64_t same = __ballot(cls == c);
-        if ((int)lane == leader) wcount[wave][c] = (uint32_t)__popcll(same);
-        if (cls == c) rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
-        pending &= ~same;
-    }
-    __syncthreads();
-    if (wave == 0) {  // offsets in (class, wave) order: lane c scans class c's total
-        uint32_t cnt[kCollideWaves];
-        uint32_t tot = 0;
-#pragma unroll
-        for (int w = 0; w < kCollideWaves; ++w) { cnt[w] = wcount[w][lane]; tot += cnt[w]; }
-        uint32_t incl = tot;
-        for (int d = 1; d < 64; d <<= 1) {
-            const uint32_t x = __shfl_up(incl, d);
-            if ((int)lane >= d) incl += x;
+    uint32_t src = t;
+    if (!__syncthreads_and(cls == cls0)) {
+        uint32_t rank = 0;  // position among the wave's lanes of this class
+        uint64_t pending = __ballot(1);
+        while (pending) {
+            const int leader = __ffsll((unsigned long long)pending) - 1;
+            const uint32_t c = __shfl(cls, leader);
+            const uint64_t same = __ballot(cls == c);
+            if ((int)lane == leader) wcount[wave][c] = (uint32_t)__popcll(same);
+            if (cls == c) rank = (uint32_t)__popcll(same & ((1ull << lane) - 1ull));
+            pending &= ~same;
         }
-        uint32_t run = incl - tot;
+        __syncthreads();
+        if (wave == 0) {  // offsets in (class, wave) order: lane c scans class c's total
+            uint32_t cnt[kCollideWaves];
+            uint32_t tot = 0;
 #pragma unroll
-        for (int w = 0; w < kCollideWaves; ++w) { wcount[w][lane] = run; run += cnt[w]; }
+            for (int w = 0; w < kCollideWaves; ++w) { cnt[w] = wcount[w][lane]; tot += cnt[w]; }
+            uint32_t incl = tot;
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t x = __shfl_up(incl, d);
+                if ((int)lane >= d) incl += x;
+            }
+            uint32_t run = incl - tot;
+#pragma unroll
+            for (int w = 0; w < kCollideWaves; ++w) { wcount[w][lane] = run; run += cnt[w]; }
+        }
+        __syncthreads();
+        order[wcount[wave][cls] + rank] = (uint16_t)t;
+        __syncthreads();
+        src = order[t];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // operand a, then operand b
+#pragma unroll
+            for (int k = 0; k < kRecQuads; ++k) stage[k * kCollideBlock + t] = q[h * kRecQuads + k];
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kRecQuads; ++k) q[h * kRecQuads + k] = stage[k * kCollideBlock + src];
+            __syncthreads();
+        }
     }
-    __syncthreads();
-    order[wcount[wave][cls] + rank] = (uint16_t)t;
-    __syncthreads();
-    const uint32_t src = order[t];
-    const size_t j = blk + src;
     Result r = miss();
-    if (j < n) {
-        if (src != t) {
-            const float4* pa = reinterpret_cast<const float4*>(a + j);
-            const float4* pb = reinterpret_cast<const float4*>(b + j);
-#pragma unroll
-            for (int k = 0; k < kRecQuads; ++k) { q[k] = pa[k]; q[kRecQuads + k] = pb[k]; }
-        }
-        r = detect(side_from(q[0], q[1], q[2], q[3]), side_from(q[4], q[5], q[6], q[7]));
-    }
+    if (blk + src < n) r = detect(side_from(q[0], q[1], q[2], q[3]), side_from(q[4], q[5], q[6], q[7]));
     float4* so = stage + src * kRecQuads;
     so[0] = make_float4(r.point.x, r.point.y, r.point.z, r.pen);
     so[1] = make_float4(r.normal.x, r.normal.y, r.normal.z, __uint_as_float(r.valid ? 1u : 0u));
