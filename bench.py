@@ -5,11 +5,12 @@ Workload: Ant, 4096 envs, MJCF timestep 0.01, substep
 4 solver iterations, 64 contacts per env; actions i.i.d. U[-1,1] per env and step (seed 0),
 torso height 0.75 + U[-0.1,0.1] and hinge noise U[-0.1,0.1] applied with reset_to_state.
 
-A "step" is one pass of World.step over all envs with that step's actions already resident
-in HBM (zeno_amd_world_step_device). W untimed warm-up steps and a reset precede K timed
-steps, bracketed by a stream synchronisation on both sides. The reference's own method
-(benchmarks/bench_full_physics.zig:67-83: zeno_world_step on host actions, so one
-host->device copy per step) is timed afterwards and reported beside value as host_actions.
+A "step" is one zeno_world_step call over all envs on that step's host actions, the
+reference's own method (benchmarks/bench_full_physics.zig:67-83). W untimed warm-up steps,
+a reset, and untimed steps until every contact list is full precede K timed steps,
+bracketed by a stream synchronisation on both sides. Beside value: the same steps with the
+actions resident in HBM, replayed from one HIP graph, and the caller's per-step loop
+(step + observations, rewards, dones).
 
 Printed: one JSON line with value = env-steps/s, a roofline object for the step kernel
 (HIP events on the library's stream over the timed region; algorithmic bytes per env-step
@@ -31,7 +32,6 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-METRIC = "env-steps/sec at Ant 4096 envs × 1000 steps; achieved HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -223,6 +223,22 @@ def bench_collide(n: int, steps: int, warmup: int, cpu_seconds: float, no_cpu: b
     return result
 
 
+def settle_steps(w, acts, limit: int = 64) -> int:
+    """Untimed steps after a reset until every env's contact list is full (the count never
+    resets, ledger Q1, so the list saturates at max_contacts within a few steps and the step
+    then does the same work every call); scenes whose counts stop growing stop early.
+    Returns the number of steps taken (actions acts[0..n))."""
+    M = w.max_contacts_per_env
+    prev = None
+    for k in range(limit):
+        counts = w.get_prev_contact_counts()  # a copy: hands out no view
+        if counts.min() >= M or (prev is not None and np.array_equal(counts, prev)):
+            return k
+        prev = counts
+        w.step(acts[k])
+    return limit
+
+
 def main() -> int:
     from zeno_amd.scenes import WORKLOADS, workload_inputs
 
@@ -237,7 +253,8 @@ def main() -> int:
     ap.add_argument("--max-contacts", type=int, default=64, help="max_contacts_per_env of the world")
     ap.add_argument("--extended-contacts", action="store_true",
                     help="extended-contact mode: box and capsule pairs through detectCollision in the step")
-    ap.add_argument("--no-host-loop", action="store_true")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the device-action, HIP-graph, env-loop and published-config legs")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay leg")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run 3 device-to-device copies of this many MiB (a plain copy kernel "
@@ -261,78 +278,99 @@ def main() -> int:
 
     wl = WORKLOADS[args.workload]
     E = args.envs or wl.num_envs
-    total = args.warmup + args.steps
+    settle_max = 64
+    total = max(args.warmup, 1) + settle_max + args.steps
     path, xml, model, state, acts = workload_inputs(args.workload, E, total, seed=0)
     w = ZenoWorld(mjcf_path=path, mjcf_string=xml, num_envs=E, max_contacts_per_env=args.max_contacts)
     if args.extended_contacts:
         w.set_extended_contacts(True)
     epw, lds = w.launch_config()
 
-    # Warm-up, then reset to the seeded initial state (bench_full_physics.zig:67-72).
+    # Warm-up, then reset to the seeded initial state (bench_full_physics.zig:67-72), then
+    # untimed steps until the contact lists are full, so that a short run times the steady
+    # state. Every leg below starts from the same reset and the same settling steps.
     w.reset_to_state(*state)
     for k in range(args.warmup):
         w.step(acts[k])
     w.reset_to_state(*state)
-    w.synchronize()
+    S = settle_steps(w, acts)
+    timed = acts[S:S + args.steps]
 
-    # Timed region (value): K steps with the actions already resident in HBM, one
-    # zeno_amd_world_step_device launch per step, bracketed by a stream synchronisation; HIP
-    # events on the world's stream around a sample of the launches give the kernel's average
-    # duration.
-    A = model["num_actuators"]
-    flat = np.ascontiguousarray(acts[args.warmup:args.warmup + args.steps]).reshape(-1)
-    if flat.size == 0:
-        flat = np.zeros(1, np.float32)
-    dptr, dfree = hip_device_buffer(flat)
-    stride = E * A * 4
+    def restart():
+        w.reset_to_state(*state)
+        for k in range(S):
+            w.step(acts[k])
+        w.synchronize()
+
+    # Timed region (value): the reference's own method, bench_full_physics.zig:67-83: K
+    # zeno_world_step calls on host actions (the kernel reads them in place from a pinned
+    # ring), wall clock between two stream synchronisations. HIP events on the world's
+    # stream around every 8th launch give the step kernel's average duration (an event pair
+    # costs a few us, so timing every launch would slow the loop it measures).
     w.synchronize()
-    # Every 8th launch is bracketed by an event pair: an event pair costs a few us per launch,
-    # so timing every launch would slow the loop it measures.
     w.set_kernel_timing(True, every=8)
     w.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
-        rc = w._lib.zeno_amd_world_step_device(w.handle, C.c_void_p(dptr + k * stride), 0)
-        if rc != 0:
-            raise RuntimeError(f"step_device failed: {rc}")
+        w.step(timed[k])
     w.synchronize()
     elapsed = time.perf_counter() - t0
     kernel_ms, launches = w.get_kernel_timing()
     w.set_kernel_timing(False)
-
-    # Third leg (reported beside value): the same K steps captured into one HIP graph
-    # (zeno_amd_world_capture_steps) from the same initial state and replayed with one call.
-    graph_leg = None
-    if not args.no_graph:
-        w.reset_to_state(*state)
-        w.synchronize()
-        w.capture_steps(dptr, stride, args.steps)
-        t2 = time.perf_counter()
-        w.graph_launch()
-        w.synchronize()
-        el3 = time.perf_counter() - t2
-        w.release_graph()
-        graph_leg = {"value": E * args.steps / el3, "ms_per_step": 1e3 * el3 / args.steps,
-                     "method": "the timed steps captured into one HIP graph and replayed with one launch call"}
-    dfree()
     value = E * args.steps / elapsed
     kernel_avg_s = (kernel_ms / 1e3) / max(launches, 1)
     pos = w.get_body_positions(zero_copy=False)
-    finite = bool(np.isfinite(pos).all())  # after the graph leg when it ran: same steps, same inputs
+    finite = bool(np.isfinite(pos).all())
 
-    # Second leg (reported beside value, never as value): the reference's own method,
-    # zeno_world_step with host actions, so the per-step host->device copy is included.
-    host_loop = None
-    if not args.no_host_loop:
-        w.reset_to_state(*state)
-        w.synchronize()
+    legs = {}
+    if not args.no_legs:
+        # Device-resident actions (zeno_amd_world_step_device): no host ring.
+        A = model["num_actuators"]
+        flat = np.ascontiguousarray(timed).reshape(-1)
+        if flat.size == 0:
+            flat = np.zeros(1, np.float32)
+        dptr, dfree = hip_device_buffer(flat)
+        stride = E * A * 4
+        restart()
         t1 = time.perf_counter()
         for k in range(args.steps):
-            w.step(acts[args.warmup + k])
+            rc = w._lib.zeno_amd_world_step_device(w.handle, C.c_void_p(dptr + k * stride), 0)
+            if rc != 0:
+                raise RuntimeError(f"step_device failed: {rc}")
         w.synchronize()
-        el2 = time.perf_counter() - t1
-        host_loop = {"value": E * args.steps / el2, "ms_per_step": 1e3 * el2 / args.steps,
-                     "method": "zeno_world_step with host actions (PCIe copy per step included)"}
+        el = time.perf_counter() - t1
+        legs["device_actions"] = {"value": E * args.steps / el, "ms_per_step": 1e3 * el / args.steps,
+                                  "method": "zeno_amd_world_step_device with the actions resident in HBM"}
+        # The same K steps captured into one HIP graph and replayed with one call.
+        if not args.no_graph:
+            restart()
+            w.capture_steps(dptr, stride, args.steps)
+            t2 = time.perf_counter()
+            w.graph_launch()
+            w.synchronize()
+            el = time.perf_counter() - t2
+            w.release_graph()
+            legs["hip_graph"] = {"value": E * args.steps / el, "ms_per_step": 1e3 * el / args.steps,
+                                 "method": "the timed steps captured into one HIP graph, replayed with one launch call"}
+        dfree()
+        # The caller's per-step loop (ZenoEnv.step, python/zeno/env.py:130-178): step, then
+        # observations, rewards and dones every step. The observation mirror is handed out by
+        # the first getter call, so every later step returns with it current: one
+        # device-to-host copy of E x obs_dim floats per step, waited for.
+        restart()
+        t3 = time.perf_counter()
+        for k in range(args.steps):
+            w.step(timed[k])
+            obs = w.get_observations()
+            w.get_rewards()
+            w.get_dones()
+        el = time.perf_counter() - t3
+        legs["env_loop"] = {"value": E * args.steps / el, "ms_per_step": 1e3 * el / args.steps,
+                            "extra_us_per_step_over_value": 1e6 * (el / args.steps - elapsed / args.steps),
+                            "obs_bytes_per_step": int(obs.nbytes),
+                            "method": "zeno_world_step on host actions + get_observations (copy) + "
+                                      "get_rewards + get_dones every step"}
+        finite = finite and bool(np.isfinite(obs).all())
 
     bytes_env_step = algorithmic_bytes_per_env_step(model, w.max_contacts_per_env)
     bytes_launch = bytes_env_step * E
@@ -342,8 +380,10 @@ def main() -> int:
     prof = ROOT / "profiles" / f"{tag}_hbm_traffic.json"
     traffic = load_traffic(prof)
 
+    metric = (f"env-steps/sec at Ant 4096 envs × {args.steps} steps; achieved HBM GB/s"
+              if args.workload == "ant" and E == 4096 else f"env-steps/sec at {args.workload} {E} envs × {args.steps} steps")
     result = {
-        "metric": METRIC if args.workload == "ant" and E == 4096 else f"env-steps/sec at {args.workload} {E} envs",
+        "metric": metric,
         "value": value,
         "unit": "env-steps/s",
         "n_gpus": 1,
@@ -356,10 +396,10 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: seeded initial-state noise and i.i.d. actions on the reference's MJCF model",
         "config": {
-            "workload": f"{args.workload} {E} envs x {args.steps} steps (actions resident in HBM)",
+            "workload": f"{args.workload} {E} envs x {args.steps} steps, zeno_world_step on host actions",
             "model": wl.mjcf, "num_envs": E, "timestep": w.timestep, "substeps": 1,
             "contact_iterations": 4, "max_contacts_per_env": w.max_contacts_per_env,
-            "envs_per_wave": epw, "lds_bytes_per_workgroup": lds,
+            "settle_steps": S, "envs_per_wave": epw, "lds_bytes_per_workgroup": lds,
             "extended_contacts": bool(args.extended_contacts), "placement": w.modes()["placement"],
         },
         "hbm_gbps": bytes_env_step * value / 1e9,
@@ -372,14 +412,14 @@ def main() -> int:
             "traffic": traffic,
             "kernel": "step_kernel",
             "kernel_avg_us": kernel_avg_s * 1e6,
+            "kernel_launches_timed": launches,
             "algorithmic_bytes_per_env_step": bytes_env_step,
             "algorithmic_bytes_per_launch": bytes_launch,
         },
-        "host_actions": host_loop,
-        "hip_graph": graph_leg,
+        **legs,
         "finite": finite,
     }
-    if args.workload == "ant" and not args.no_host_loop:
+    if args.workload == "ant" and not args.no_legs:
         result["published_configs"] = {
             "note": "the reference's own benchmark method and configs (1024 envs, dt 0.002, host actions, "
                     "1000 steps) on this GPU, beside its published Apple M4 Pro numbers",

@@ -74,6 +74,9 @@ def load() -> C.CDLL:
         lib.zo_asinf.argtypes = [C.c_float]
         lib.zo_match_cached.restype = None
         lib.zo_match_cached.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32]
+        lib.zo_solve_contact_slot.restype = None
+        lib.zo_solve_contact_slot.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                              C.c_float, C.c_float, C.c_float]
         lib.zo_sort_contacts.restype = None
         lib.zo_sort_contacts.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32]
         lib.zo_detect_collision.restype = C.c_int
@@ -253,6 +256,21 @@ def match_cached(contacts: np.ndarray, count: int, prev: np.ndarray, prev_count:
     """In-place warm start of one env's contacts from its previous list."""
     assert contacts.shape == prev.shape
     load().zo_match_cached(contacts.shape[0], _p(contacts), count, _p(prev), prev_count)
+
+
+def solve_contact_slot(inv_mass_inertia: np.ndarray, positions: np.ndarray, velocities: np.ndarray,
+                       angular_velocities: np.ndarray, contact: np.ndarray, baumgarte: float = 0.2,
+                       slop: float = 0.005, dt: float = 0.01) -> None:
+    """solve_contacts on one slot (all_shaders.metal:1644-1793). The [B, 4] float32 state
+    arrays and the one-record contact array are updated in place."""
+    arrs = [np.ascontiguousarray(x, np.float32) for x in (inv_mass_inertia, positions, velocities, angular_velocities)]
+    for x, orig in zip(arrs[1:], (positions, velocities, angular_velocities)):
+        assert x is orig, "state arrays must be C-contiguous float32 (updated in place)"
+    assert contact.dtype == CONTACT_DTYPE and contact.shape == (1,) and contact.flags["C_CONTIGUOUS"]
+    B = arrs[0].shape[0]
+    assert all(x.shape == (B, 4) for x in arrs)
+    load().zo_solve_contact_slot(B, _p(arrs[0]), _p(positions), _p(velocities), _p(angular_velocities), _p(contact),
+                                 baumgarte, slop, dt)
 
 
 def collide_env(world: "OracleWorld", env: int = 0) -> None:

@@ -1054,6 +1054,31 @@ void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,
     k_match_cached(&e);
 }
 
+/* solve_contacts (all_shaders.metal:1644-1793) on one slot, exposed for unit tests: the
+ * slot's bodies index [num_bodies] records of inverse mass and inertia, positions,
+ * velocities and angular velocities (4 floats each), updated in place with the slot. */
+void zo_solve_contact_slot(uint32_t num_bodies, const float* inv_mass_inertia, float* positions, float* velocities,
+                           float* angular_velocities, ZoContact* contact, float baumgarte, float slop, float dt) {
+    ZoModel m;
+    Env e;
+    uint32_t count = 1;
+    memset(&m, 0, sizeof m);
+    memset(&e, 0, sizeof e);
+    m.baumgarte = baumgarte;
+    m.slop = slop;
+    e.m = &m;
+    e.B = num_bodies;
+    e.M = 1;
+    e.dt = dt;
+    e.invmi = (float*)inv_mass_inertia;
+    e.pos = positions;
+    e.vel = velocities;
+    e.angvel = angular_velocities;
+    e.con = contact;
+    e.count = &count;
+    solve_contact(&e, 0);
+}
+
 void zo_broad_phase_hash(const ZoModel* m, const float* positions, uint32_t* cell_ids,
                          ZoContact* contacts, uint32_t* count) {
     k_broad_phase_hash(m, positions, cell_ids, contacts, count);

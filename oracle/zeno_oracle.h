@@ -141,6 +141,13 @@ void zo_detect_collisions(const ZoCollider* a, const ZoCollider* b, uint32_t n, 
 void zo_match_cached(uint32_t max_contacts, ZoContact* contacts, uint32_t count,
                      ZoContact* prev_contacts, uint32_t prev_count);
 
+/* solve_contacts (all_shaders.metal:1644-1793) on one slot, exposed for unit tests: the
+ * slot's body indices address [num_bodies] float4 records of inverse mass and inertia,
+ * positions, velocities and angular velocities; state and contact->impulses[0] are updated
+ * in place. */
+void zo_solve_contact_slot(uint32_t num_bodies, const float* inv_mass_inertia, float* positions, float* velocities,
+                           float* angular_velocities, ZoContact* contact, float baumgarte, float slop, float dt);
+
 /* sort_contacts (all_shaders.metal:711-745) on one env's list, exposed for unit tests. */
 void zo_sort_contacts(uint32_t max_contacts, ZoContact* contacts, uint32_t count);
 

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from oracle.oracle import OracleWorld
-from tests.parity import compare, gpu_arrays, make_pair, oracle_arrays
+from tests.parity import compare, gpu_arrays, live_mask, make_pair, oracle_arrays
 from zeno_amd.model import load_model
 from zeno_amd.scenes import ASSETS
 from zeno_amd.world import ZenoWorld
@@ -94,10 +94,46 @@ def test_zero_copy_views():
         snap = p1.copy()
         for _ in range(5):
             w.step(np.ones((2, 1), np.float32))
-        w.get_body_positions()  # a getter call refreshes the mirror in place
+        # no getter call in between: the held view shows the stepped state
         assert not np.array_equal(p1, snap)
         raw = w._lib.zeno_world_get_body_positions(w.handle)
         assert C.addressof(raw.contents) == p1.ctypes.data
+
+
+def test_held_views_follow_every_state_change():
+    """Views taken once stay current across step, step_subset, reset, reset_to_state and the
+    setters (the reference's shared-memory buffers do), and match the oracle after steps."""
+    E = 6
+    g, o, acts = make_pair("ant", E, 6, seed=5)
+    views = {"positions": g.get_body_positions(), "quaternions": g.get_body_quaternions(),
+             "velocities": g.get_body_velocities(), "angular_velocities": g.get_body_angular_velocities(),
+             "joint_positions": g.get_joint_positions(), "observations": g.get_sensor_data()}
+    con = g.get_contacts()
+    for k in range(4):
+        g.step(acts[k])
+        o.step(acts[k])
+    for name, v in views.items():
+        np.testing.assert_array_equal(v, getattr(o, name)[:, : v.shape[1]] if v.ndim == 2 else getattr(o, name), name)
+    live = live_mask(o.contact_counts, g.max_contacts_per_env)
+    np.testing.assert_array_equal(con["indices"][live], o.contacts["indices"][live])
+    np.testing.assert_array_equal(con["position_pen"][live], o.contacts["position_pen"][live])
+    mask = np.zeros(E, np.uint8)
+    mask[::2] = 1
+    g.step_subset(acts[4], mask)
+    o.step_subset(acts[4], mask)
+    np.testing.assert_array_equal(views["positions"], o.positions)
+    np.testing.assert_array_equal(views["observations"], o.observations)
+    g.reset(mask)
+    o.reset(mask)
+    np.testing.assert_array_equal(views["positions"], o.positions)
+    np.testing.assert_array_equal(views["joint_positions"], o.joint_positions[:, : g.num_joints])
+    p = o.positions.copy()
+    p[:, 1, 2] += 0.25
+    g.set_body_positions(p)
+    np.testing.assert_array_equal(views["positions"], p)
+    q = o.quaternions.copy()
+    g.reset_to_state(p, q, np.zeros_like(p), np.zeros_like(p))
+    np.testing.assert_array_equal(views["velocities"], 0.0)
 
 
 def test_step_subset_matches_reference_semantics():

@@ -495,3 +495,27 @@ def test_motor_torque_closed_form():
     np.testing.assert_allclose(w.joint_velocities[0, 0], 2 * np.sin(theta / 2) / 0.01, rtol=1e-4)
     np.testing.assert_allclose(w.observations[0, :2], [w.joint_positions[0, 0], w.joint_velocities[0, 0]])
     np.testing.assert_allclose(w.joint_torques[0, 0], 2.0)
+
+
+def test_kinematic_body_closed_form():
+    """update_kinematic (all_shaders.metal:304-339) on a body of type 1, which the reference
+    builds with zero inverse mass and inertia (body.zig:53-75; MJCF never yields one, so the
+    record is edited here): each substep moves it by v dt and turns it by 2 atan(w dt / 2)
+    about its spin axis; gravity, integration and the velocity update leave it alone."""
+    m = load_model(mjcf_string=FREE_NO_PLANE)
+    m["bodies"]["params"][1, 1] = 1.0
+    m["inv_mass_inertia"][1] = 0.0
+    w = O.OracleWorld(m, 1)
+    v = w.velocities.copy()
+    v[0, 1, :3] = [0.5, -0.2, 0.1]
+    av = w.angular_velocities.copy()
+    av[0, 1, :3] = [0.0, 0.0, 3.0]
+    w.reset_to_state(w.positions.copy(), w.quaternions.copy(), v, av)
+    for _ in range(5):
+        w.step(None)
+    np.testing.assert_allclose(w.positions[0, 1, :3], 5 * 0.01 * np.array([0.5, -0.2, 0.1]), rtol=1e-5)
+    np.testing.assert_allclose(_angle_about(w.quaternions[0, 1], [0, 0, 1]), 5 * 2 * np.arctan(3.0 * 0.01 / 2),
+                               rtol=1e-5)
+    np.testing.assert_array_equal(w.velocities[0, 1, :3], np.float32([0.5, -0.2, 0.1]))
+    np.testing.assert_array_equal(w.angular_velocities[0, 1, :3], np.float32([0.0, 0.0, 3.0]))
+    np.testing.assert_array_equal(w.torques[0, 1], 0.0)

@@ -832,17 +832,12 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
         }
         __syncthreads();
-        // ---- B: compute_forces + update_kinematic (:345-388, :304-339) ----------------
+        // ---- B: compute_forces, then update_kinematic (:345-388, :304-339) ----------
+        // In dispatch order (world.zig:962-990): the torque reads the quaternion before a
+        // kinematic body's update.
         if (live) {
             for (uint32_t b = sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
-                if (md.flags[b] & 1u) {
-                    f3 p = add(xyz(s.pos[b]), scale(xyz(s.vel[b]), a.dt));
-                    s.pos[b] = tof4(p, 0.0f);
-                    q4 q = toq(s.quat[b]);
-                    f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
-                    s.quat[b] = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
-                }
                 if (imi.x < 1e-8f) {
                     s.frc[b] = make_float4(0, 0, 0, 0);
                     s.trq[b] = make_float4(0, 0, 0, 0);
@@ -852,6 +847,13 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     s.frc[b] = tof4(force, 0.0f);
                     f3 cw = qrot(xyz(md.com[b]), toq(s.quat[b]));
                     s.trq[b] = tof4(cross(cw, force), 0.0f);
+                }
+                if (md.flags[b] & 1u) {
+                    f3 p = add(xyz(s.pos[b]), scale(xyz(s.vel[b]), a.dt));
+                    s.pos[b] = tof4(p, 0.0f);
+                    q4 q = toq(s.quat[b]);
+                    f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
+                    s.quat[b] = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
                 }
             }
         }

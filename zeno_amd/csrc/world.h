@@ -11,7 +11,10 @@
 
 namespace za {
 
-// Host mirror ids (one pinned buffer each, refreshed lazily after device work).
+// Host mirror ids: one pinned host buffer each. A mirror whose pointer a getter has handed
+// out ("exposed") is brought up to date before every call that changes device state returns,
+// so a view the caller holds follows the simulation like the reference's shared-memory
+// buffers; the others are refreshed when their getter is next called.
 enum MirrorId {
     MIR_POS, MIR_QUAT, MIR_VEL, MIR_ANGVEL, MIR_ACC, MIR_JPOS, MIR_JVEL, MIR_JTRQ, MIR_OBS,
     MIR_CON, MIR_COUNT, MIR_COUNT_ALL
@@ -56,10 +59,14 @@ struct World {
     uint8_t* d_mask = nullptr;
     float4* d_stage = nullptr;  // [E*B] staging for masked state writes
 
-    // Host mirrors.
+    // Host mirrors. Exposed mirrors are refreshed by device-to-host copies on view_stream,
+    // which waits for the step stream through view_evt.
     void* h_mirror[MIR_COUNT_ALL] = {};
     size_t mirror_bytes[MIR_COUNT_ALL] = {};
     bool dirty[MIR_COUNT_ALL] = {};
+    bool exposed[MIR_COUNT_ALL] = {};
+    hipStream_t view_stream = nullptr;
+    hipEvent_t view_evt = nullptr;
     float* h_rewards = nullptr;
     uint8_t* h_dones = nullptr;
 
@@ -104,7 +111,12 @@ struct World {
     hipError_t reset_to_state(const float* pos, const float* quat, const float* vel, const float* angvel,
                               const uint8_t* mask);
     hipError_t set_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask);
-    void* mirror(MirrorId id);
+    // Host mirror of `id`, current with the device. expose: the pointer goes to a caller, who
+    // may hold it across later steps (internal reads pass false).
+    void* mirror(MirrorId id, bool expose = true);
+    // Brings every exposed mirror up to date after device work; returns once the copies are
+    // done. A no-op when no mirror has been handed out.
+    hipError_t refresh_views();
     hipError_t sync();
     hipError_t get_profiling(ZenoProfilingData* out);
     hipError_t kernel_timing(double* ms, uint64_t* launches);
@@ -119,6 +131,8 @@ struct World {
     hipError_t mark_actions_used();
     hipError_t upload_mask(const uint8_t* mask, uint8_t** d_out);
     hipError_t ensure_subset_buffers();
+    hipError_t write_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask);
+    const void* device_src(MirrorId id) const;
     void mark_all_dirty();
 };
 

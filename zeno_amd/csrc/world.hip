@@ -3,7 +3,9 @@
 // Mirrors World in src/world/world.zig: init (:215-691), step (:694-792), stepSubset
 // (:833-929), reset (:1296-1314), setters (:1413-1478), and the reset_to_state path of
 // src/main.zig:290-385. State stays in HBM; host pointers handed to callers are pinned
-// mirrors refreshed on demand.
+// mirrors. Once handed out, a mirror is refreshed before every state-changing call returns
+// (the reference's buffers are shared memory that World.step has finished writing when it
+// returns, world.zig:733); the others are refreshed when their getter is called.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -102,6 +104,9 @@ World::~World() {
     if (h_mask_stage) hipHostFree(h_mask_stage);
     std::free(h_rewards);
     std::free(h_dones);
+    if (view_stream) hipStreamSynchronize(view_stream);
+    if (view_evt) hipEventDestroy(view_evt);
+    if (view_stream) hipStreamDestroy(view_stream);
     if (prof_start) hipEventDestroy(prof_start);
     if (prof_stop) hipEventDestroy(prof_stop);
     for (hipEvent_t ev : t_events) hipEventDestroy(ev);
@@ -232,6 +237,8 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->epw = epw;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
+    if ((e = hipStreamCreateWithFlags(&w->view_stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
+    if ((e = hipEventCreateWithFlags(&w->view_evt, hipEventDisableTiming)) != hipSuccess) return fail("hipEventCreate", e);
 
     // Model blob: every per-scene record the kernel reads, packed per ModelLayout.
     w->ml = ML;
@@ -425,7 +432,7 @@ hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_
     else if (A > 0) { ZA_TRY(stage_actions(actions, &d_act)); staged = true; }
     ZA_TRY(launch(d_act, actual, nullptr));
     if (staged) ZA_TRY(mark_actions_used());
-    return hipSuccess;
+    return refresh_views();
 }
 
 void World::release_graph() {
@@ -478,7 +485,7 @@ hipError_t World::graph_launch() {
     ZA_TRY(hipSetDevice(device));
     ZA_TRY(hipGraphLaunch(graph_exec, stream));
     mark_all_dirty();
-    return hipSuccess;
+    return refresh_views();
 }
 
 hipError_t World::ensure_subset_buffers() {
@@ -520,7 +527,7 @@ hipError_t World::step_subset(const float* actions, const uint8_t* mask, uint32_
     ZA_TRY(upload_mask(mask, &dm));
     ZA_TRY(launch(d_act, actual, dm));
     if (staged) ZA_TRY(mark_actions_used());
-    return hipSuccess;
+    return refresh_views();
 }
 
 // World.reset, world.zig:1296-1314: restore the selected envs, then zero every env's
@@ -535,10 +542,15 @@ hipError_t World::reset(const uint8_t* mask) {
     ZA_TRY(hipGetLastError());
     ZA_TRY(fill_u32(stream, d_counts, E, 0));
     mark_all_dirty();
-    return hipSuccess;
+    return refresh_views();
 }
 
 hipError_t World::set_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask) {
+    ZA_TRY(write_state_array(dst, mid, src, mask));
+    return refresh_views();
+}
+
+hipError_t World::write_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask) {
     const size_t bytes = (size_t)E * B * 16;
     if (!mask) {
         ZA_TRY(hipStreamSynchronize(stream));
@@ -562,38 +574,61 @@ hipError_t World::set_state_array(float4* dst, MirrorId mid, const float* src, c
 hipError_t World::reset_to_state(const float* pos, const float* quat, const float* vel, const float* angvel,
                                  const uint8_t* mask) {
     ZA_TRY(hipSetDevice(device));
-    ZA_TRY(set_state_array(d_pos, MIR_POS, pos, mask));
-    ZA_TRY(set_state_array(d_quat, MIR_QUAT, quat, mask));
-    if (vel) ZA_TRY(set_state_array(d_vel, MIR_VEL, vel, mask));
-    if (angvel) ZA_TRY(set_state_array(d_angvel, MIR_ANGVEL, angvel, mask));
+    ZA_TRY(write_state_array(d_pos, MIR_POS, pos, mask));
+    ZA_TRY(write_state_array(d_quat, MIR_QUAT, quat, mask));
+    if (vel) ZA_TRY(write_state_array(d_vel, MIR_VEL, vel, mask));
+    if (angvel) ZA_TRY(write_state_array(d_angvel, MIR_ANGVEL, angvel, mask));
     ZA_TRY(fill_u32(stream, d_counts, E, 0));
     dirty[MIR_COUNT] = true;
-    return hipSuccess;
+    return refresh_views();
 }
 
-void* World::mirror(MirrorId id) {
-    if (hipSetDevice(device) != hipSuccess) return nullptr;
+const void* World::device_src(MirrorId id) const {
+    switch (id) {
+        case MIR_POS: return d_pos;
+        case MIR_QUAT: return d_quat;
+        case MIR_VEL: return d_vel;
+        case MIR_ANGVEL: return d_angvel;
+        case MIR_ACC: return d_acc;
+        case MIR_JPOS: return d_jpos;
+        case MIR_JVEL: return d_jvel;
+        case MIR_JTRQ: return d_jtrq;
+        case MIR_OBS: return d_obs;
+        case MIR_CON: return d_con;
+        case MIR_COUNT: return d_counts;
+        default: return nullptr;
+    }
+}
+
+void* World::mirror(MirrorId id, bool expose) {
+    if (id < 0 || id >= MIR_COUNT_ALL || hipSetDevice(device) != hipSuccess) return nullptr;
     if (dirty[id]) {
-        void* src = nullptr;
-        switch (id) {
-            case MIR_POS: src = d_pos; break;
-            case MIR_QUAT: src = d_quat; break;
-            case MIR_VEL: src = d_vel; break;
-            case MIR_ANGVEL: src = d_angvel; break;
-            case MIR_ACC: src = d_acc; break;
-            case MIR_JPOS: src = d_jpos; break;
-            case MIR_JVEL: src = d_jvel; break;
-            case MIR_JTRQ: src = d_jtrq; break;
-            case MIR_OBS: src = d_obs; break;
-            case MIR_CON: src = d_con; break;
-            case MIR_COUNT: src = d_counts; break;
-            default: return nullptr;
-        }
-        if (hipMemcpyAsync(h_mirror[id], src, mirror_bytes[id], hipMemcpyDeviceToHost, stream) != hipSuccess) return nullptr;
+        if (hipMemcpyAsync(h_mirror[id], device_src(id), mirror_bytes[id], hipMemcpyDeviceToHost, stream) != hipSuccess)
+            return nullptr;
         if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
         dirty[id] = false;
     }
+    if (expose) exposed[id] = true;
     return h_mirror[id];
+}
+
+// The copies run on view_stream behind an event of the step stream, and the call waits for
+// them: a held view must show the state the call produced when the call returns.
+hipError_t World::refresh_views() {
+    bool any = false;
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) any = any || (exposed[i] && dirty[i]);
+    if (!any) return hipSuccess;
+    ZA_TRY(hipEventRecord(view_evt, stream));
+    ZA_TRY(hipStreamWaitEvent(view_stream, view_evt, 0));
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) {
+        if (!(exposed[i] && dirty[i])) continue;
+        ZA_TRY(hipMemcpyAsync(h_mirror[i], device_src((MirrorId)i), mirror_bytes[i], hipMemcpyDeviceToHost, view_stream));
+    }
+    ZA_TRY(hipStreamSynchronize(view_stream));
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) {
+        if (exposed[i]) dirty[i] = false;
+    }
+    return hipSuccess;
 }
 
 hipError_t World::get_profiling(ZenoProfilingData* out) {
@@ -611,7 +646,7 @@ hipError_t World::get_profiling(ZenoProfilingData* out) {
         prof.collision_broad_ns = (float)((double)t[PH_BROAD] * ns);
         prof.collision_narrow_ns = (float)((double)t[PH_NARROW] * ns);
         prof.constraint_solve_ns = (float)((double)(t[PH_JOINTS] + t[PH_CONTACTS]) * ns);
-        const uint32_t* counts = (const uint32_t*)mirror(MIR_COUNT);
+        const uint32_t* counts = (const uint32_t*)mirror(MIR_COUNT, false);
         uint64_t total = 0;
         if (counts) for (uint32_t e = 0; e < E; ++e) total += counts[e];
         prof.num_contacts = (uint32_t)std::min<uint64_t>(total, 0xFFFFFFFFull);

@@ -250,16 +250,16 @@ class ZenoVectorEnv(_VectorEnv):
         self.close_extras()
 
     def get_body_positions(self, zero_copy: bool = True) -> np.ndarray:
-        return self._env._world.get_body_positions(zero_copy=zero_copy)
+        return self._env.world.get_body_positions(zero_copy=zero_copy)
 
     def get_body_quaternions(self, zero_copy: bool = True) -> np.ndarray:
-        return self._env._world.get_body_quaternions(zero_copy=zero_copy)
+        return self._env.world.get_body_quaternions(zero_copy=zero_copy)
 
     def get_state(self) -> Dict[str, np.ndarray]:
-        return self._env._world.get_state()
+        return self._env.world.get_state()
 
     def set_state(self, state: Dict[str, np.ndarray]) -> None:
-        self._env._world.set_state(state)
+        self._env.world.set_state(state)
 
 
 def register_envs() -> None:

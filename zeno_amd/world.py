@@ -2,9 +2,10 @@
 
 Method names, argument meanings, array shapes and error behaviour follow the reference's
 ZenoWorld. Arrays returned with ``zero_copy=True`` are views of the library's pinned host
-mirrors; the mirror behind a view is refreshed from the GPU each time its getter is called
-after a step, so a view obtained earlier shows the new values once the getter has been
-called again (the reference's unified-memory views update without that call).
+mirrors. Once a getter has handed a mirror out, the library brings it up to date before
+every step, reset or setter returns, so a view held across steps follows the simulation as
+the reference's unified-memory views do (at the cost of one device-to-host copy of that
+array per call; arrays never handed out are copied only when their getter is called).
 """
 from __future__ import annotations
 
