@@ -319,10 +319,11 @@ def main() -> int:
     w.set_kernel_timing(False)
     value = E * args.steps / elapsed
     kernel_avg_s = (kernel_ms / 1e3) / max(launches, 1)
-    pos = w.get_body_positions(zero_copy=False)
-    finite = bool(np.isfinite(pos).all())
+    # No getter touches this world before the legs are done: a getter hands its array out,
+    # and every later step would then store that array to host memory as well.
 
     legs = {}
+    finite = True
     if not args.no_legs:
         # Device-resident actions (zeno_amd_world_step_device): no host ring.
         A = model["num_actuators"]
@@ -370,7 +371,8 @@ def main() -> int:
                             "obs_bytes_per_step": int(obs.nbytes),
                             "method": "zeno_world_step on host actions + get_observations (copy) + "
                                       "get_rewards + get_dones every step"}
-        finite = finite and bool(np.isfinite(obs).all())
+        finite = bool(np.isfinite(obs).all())
+    finite = finite and bool(np.isfinite(w.get_body_positions(zero_copy=False)).all())
 
     bytes_env_step = algorithmic_bytes_per_env_step(model, w.max_contacts_per_env)
     bytes_launch = bytes_env_step * E

@@ -38,6 +38,7 @@ struct EnvLds {
     // Candidate-pair broad phase with the model records in HBM: each geom's local centre and
     // radius (float4[G]) and body | type << 16 (u32[G]), staged once per launch.
     uint32_t gst, gmeta;
+    uint32_t obs;                                                      // float[obs']: the observation row
     uint32_t misc;                                                     // u32[4]: count, pcount, nlev, pad
     uint32_t bytes;                                                    // total, multiple of 16
 };
@@ -61,7 +62,7 @@ inline uint32_t hash_bytes_for(uint32_t G, bool staged) {
 // G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
 // solve records when they are copied per environment (HBM working set), else 0.
 inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint32_t G = 0, uint32_t jrec_bytes = 0,
-                           bool stage_geoms = false) {
+                           bool stage_geoms = false, uint32_t obsp = 1) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
@@ -87,6 +88,7 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.jrec = take(jrec_bytes);
     if (8 * mask_words > 32) L.bmask = take(8 * mask_words * B);
     if (stage_geoms) { L.gst = take(16 * G); L.gmeta = take(4 * G); }
+    L.obs = take(4 * obsp);
     L.misc = take(16);
     L.bytes = o;
     return L;
@@ -299,6 +301,15 @@ struct StepArgs {
     float* jpos; float* jvel; float* jtrq;                                // [E*J']
     float* obs;                                                           // [E*obs']
     float* lam;                                                           // [E*N]
+    // Device addresses of the host mirrors a caller holds (mapped pinned memory), else null:
+    // the write-back stores each of these arrays there as well as to HBM, so a held view is
+    // current when the stream completes, without a separate copy.
+    struct HostViews {
+        float4 *pos, *quat, *vel, *angvel, *acc;
+        float *jpos, *jvel, *jtrq, *obs;
+        ContactRec* contacts;
+        uint32_t* counts;
+    } hv;
     const float* actions;                                                 // [E*A]
     ContactRec* contacts;                                                 // [E*M]
     uint32_t* counts; uint32_t* pcounts;                                  // [E]

@@ -49,6 +49,7 @@ struct Lds {
     float4* jrec;            // per-environment solve records (model records in HBM)
     float4* gst;             // staged geom local centre + radius (model records in HBM, no hash)
     uint32_t* gmeta;         // staged geom body | type << 16
+    float* obs;              // the observation row (stage L), written back with the state
     uint32_t* misc;
 };
 
@@ -79,6 +80,7 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.jrec = (float4*)(base + L.jrec);
     s.gst = (float4*)(base + L.gst);
     s.gmeta = (uint32_t*)(base + L.gmeta);
+    s.obs = (float*)(base + L.obs);
     s.misc = (uint32_t*)(base + L.misc);
     return s;
 }
@@ -1461,8 +1463,12 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         }
         __syncthreads();
         // ---- L: read_sensors (:1799-1893); cache_contacts is the next snapshot --------
+        // The row is assembled in the working set and written back with the state. Entries
+        // that no sensor writes are 0 (nothing else ever writes the observation buffer).
         if (stepped && step + 1 == a.substeps) {
-            float* obs = a.obs + (size_t)env * a.obsp;
+            float* obs = s.obs;
+            for (uint32_t k = sl; k < a.obsp; k += G) obs[k] = 0.0f;
+            wave_sync<HBM>();
             for (uint32_t k = sl; k < a.S; k += G) {
                 const SensorRec& sr = md.sensors[k];
                 const uint32_t obj = sr.type_object[1];
@@ -1493,27 +1499,50 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     const uint32_t n_out = count < M ? count : M;
     if (stepped) {
         const size_t eb = (size_t)env * B;
+        const StepArgs::HostViews& hv = a.hv;
         for (uint32_t b = sl; b < B; b += G) {
-            a.pos[eb + b] = s.pos[b];
-            a.quat[eb + b] = s.quat[b];
-            const float4 v = s.vel[b], v0 = s.vb[b];
+            const float4 p = s.pos[b], q = s.quat[b], v = s.vel[b], v0 = s.vb[b], w = s.angvel[b];
+            const float4 acc = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+            a.pos[eb + b] = p;
+            a.quat[eb + b] = q;
             a.vel[eb + b] = v;
-            a.angvel[eb + b] = s.angvel[b];
-            a.acc[eb + b] = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+            a.angvel[eb + b] = w;
+            a.acc[eb + b] = acc;
+            if (hv.pos) hv.pos[eb + b] = p;
+            if (hv.quat) hv.quat[eb + b] = q;
+            if (hv.vel) hv.vel[eb + b] = v;
+            if (hv.angvel) hv.angvel[eb + b] = w;
+            if (hv.acc) hv.acc[eb + b] = acc;
         }
         for (uint32_t j = sl; j < a.J; j += G) {
             const size_t o = (size_t)env * Jp + j;
             a.jtrq[o] = s.jt[j];
             a.jpos[o] = s.jp[j];
             a.jvel[o] = s.jv[j];
+            if (hv.jtrq) hv.jtrq[o] = s.jt[j];
+            if (hv.jpos) hv.jpos[o] = s.jp[j];
+            if (hv.jvel) hv.jvel[o] = s.jv[j];
+        }
+        for (uint32_t k = sl; k < a.obsp; k += G) {
+            const size_t o = (size_t)env * a.obsp + k;
+            a.obs[o] = s.obs[k];
+            if (hv.obs) hv.obs[o] = s.obs[k];
         }
         ContactRec* gc = a.contacts + (size_t)env * M;
         for (uint32_t k = sl; k < n_out; k += G) {
             const float4* src = (const float4*)&s.con[s.perm[k]];
+            const float4 c0 = src[0], c1 = src[1], c2 = src[2], c3 = src[3];
             float4* d = (float4*)&gc[k];
-            d[0] = src[0]; d[1] = src[1]; d[2] = src[2]; d[3] = src[3];
+            d[0] = c0; d[1] = c1; d[2] = c2; d[3] = c3;
+            if (hv.contacts) {
+                float4* h = (float4*)&hv.contacts[(size_t)env * M + k];
+                h[0] = c0; h[1] = c1; h[2] = c2; h[3] = c3;
+            }
         }
-        if (sl == 0) a.counts[env] = count;
+        if (sl == 0) {
+            a.counts[env] = count;
+            if (hv.counts) hv.counts[env] = count;
+        }
     } else {
         // Not advanced: keep visible state, record the advanced contact list as the
         // previous-contact snapshot (world.zig:880-928 restores everything else).

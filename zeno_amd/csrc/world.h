@@ -65,6 +65,8 @@ struct World {
     size_t mirror_bytes[MIR_COUNT_ALL] = {};
     bool dirty[MIR_COUNT_ALL] = {};
     bool exposed[MIR_COUNT_ALL] = {};
+    void* d_view[MIR_COUNT_ALL] = {};  // device addresses of the mirrors (mapped pinned memory)
+    bool views_pending = false;        // the last launch stores held views; wait for the stream
     hipStream_t view_stream = nullptr;
     hipEvent_t view_evt = nullptr;
     float* h_rewards = nullptr;

@@ -153,7 +153,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
 
     w->hash = m.num_geoms > kHashMinGeoms;
     if (w->hash && m.num_geoms > kHashMaxGeoms) { err = "scene too large for the spatial hash (over 16384 geoms)"; delete w; return nullptr; }
-    EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms);
+    EnvLds L = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 0, false, w->obsp);
     std::vector<float4> invmi(w->B), com(w->B);
     std::vector<uint32_t> flags(w->B);
     for (uint32_t b = 0; b < w->B; ++b) {
@@ -183,7 +183,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
     const EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash);
     const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec,
-                                      !w->hash);
+                                      !w->hash, w->obsp);
     struct Cand { uint32_t pl; int epw; size_t shmem; };
     std::vector<Cand> cands;
     int force_pl = -1, force_epw = 0;
@@ -307,14 +307,17 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
                        w->d_init_angvel, w->d_pos, w->d_quat, w->d_vel, w->d_angvel, w->d_jpos, w->d_jvel);
     if ((e = hipGetLastError()) != hipSuccess) return fail("init kernel", e);
 
-    // Host mirrors.
+    // Host mirrors: pinned, mapped and coherent, so that the step kernel can store the
+    // arrays a caller holds straight into them (StepArgs::hv).
     const size_t mb[MIR_COUNT_ALL] = {EB * 16, EB * 16, EB * 16, EB * 16, EB * 16,
                                       (size_t)w->E * w->Jp * 4, (size_t)w->E * w->Jp * 4, (size_t)w->E * w->Jp * 4,
                                       (size_t)w->E * w->obsp * 4, (size_t)w->E * std::max<uint32_t>(w->M, 1) * 64,
                                       (size_t)w->E * 4};
     for (int i = 0; i < MIR_COUNT_ALL; ++i) {
         w->mirror_bytes[i] = mb[i];
-        if ((e = hipHostMalloc(&w->h_mirror[i], mb[i], hipHostMallocDefault)) != hipSuccess) return fail("hipHostMalloc", e);
+        if ((e = hipHostMalloc(&w->h_mirror[i], mb[i], hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess)
+            return fail("hipHostMalloc", e);
+        if ((e = hipHostGetDevicePointer(&w->d_view[i], w->h_mirror[i], 0)) != hipSuccess) return fail("hipHostGetDevicePointer", e);
         w->dirty[i] = true;
     }
     w->h_rewards = (float*)std::calloc(w->E, sizeof(float));
@@ -372,14 +375,31 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.prev_detached_out = d_prev_detached;
     a.lds = lds;
     a.lds_small = lds_small;
+    // Held views are stored by the kernel itself in eager launches; a captured launch keeps
+    // the views of capture time, so graph_launch refreshes them by copies instead.
+    const bool direct = !capturing;
+    auto view = [&](MirrorId id) { return direct && exposed[id] ? d_view[id] : nullptr; };
+    a.hv.pos = (float4*)view(MIR_POS);
+    a.hv.quat = (float4*)view(MIR_QUAT);
+    a.hv.vel = (float4*)view(MIR_VEL);
+    a.hv.angvel = (float4*)view(MIR_ANGVEL);
+    a.hv.acc = (float4*)view(MIR_ACC);
+    a.hv.jpos = (float*)view(MIR_JPOS);
+    a.hv.jvel = (float*)view(MIR_JVEL);
+    a.hv.jtrq = (float*)view(MIR_JTRQ);
+    a.hv.obs = (float*)view(MIR_OBS);
+    a.hv.contacts = (ContactRec*)view(MIR_CON);
+    a.hv.counts = (uint32_t*)view(MIR_COUNT);
     hipEvent_t t0 = nullptr, t1 = nullptr;
     // Under capture the launch becomes a graph node; event timing and profiling stay eager-only.
     const bool timed = !capturing && timing > 0 && (t_launch++ % (uint64_t)timing) == 0;
     const bool prof_events = profiling && !capturing;
     if (timed) {
         while (t_events.size() < t_used + 2) {
+            // Timing only: no system-scope fence (cache write-back) when the event completes,
+            // which would add its own cost to the interval measured.
             hipEvent_t ev;
-            ZA_TRY(hipEventCreate(&ev));
+            ZA_TRY(hipEventCreateWithFlags(&ev, hipEventDisableSystemFence));
             t_events.push_back(ev);
         }
         t0 = t_events[t_used];
@@ -395,6 +415,12 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     if (prof_events) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
     if (timed) ZA_TRY(hipEventRecord(t1, stream));
     mark_all_dirty();
+    // The held views were current before this launch (every state-changing call leaves them
+    // so) and the kernel stores what it changes in them: they are current once the stream
+    // reaches this point.
+    for (int i = 0; i < MIR_COUNT_ALL; ++i) {
+        if (direct && exposed[i]) { dirty[i] = false; views_pending = true; }
+    }
     return hipSuccess;
 }
 
@@ -602,6 +628,10 @@ const void* World::device_src(MirrorId id) const {
 
 void* World::mirror(MirrorId id, bool expose) {
     if (id < 0 || id >= MIR_COUNT_ALL || hipSetDevice(device) != hipSuccess) return nullptr;
+    if (views_pending) {
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+        views_pending = false;
+    }
     if (dirty[id]) {
         if (hipMemcpyAsync(h_mirror[id], device_src(id), mirror_bytes[id], hipMemcpyDeviceToHost, stream) != hipSuccess)
             return nullptr;
@@ -617,7 +647,15 @@ void* World::mirror(MirrorId id, bool expose) {
 hipError_t World::refresh_views() {
     bool any = false;
     for (int i = 0; i < MIR_COUNT_ALL; ++i) any = any || (exposed[i] && dirty[i]);
-    if (!any) return hipSuccess;
+    if (!any) {
+        // Views the step kernel stored itself are current once the stream is done.
+        if (views_pending) {
+            ZA_TRY(hipStreamSynchronize(stream));
+            views_pending = false;
+        }
+        return hipSuccess;
+    }
+    views_pending = false;
     ZA_TRY(hipEventRecord(view_evt, stream));
     ZA_TRY(hipStreamWaitEvent(view_stream, view_evt, 0));
     for (int i = 0; i < MIR_COUNT_ALL; ++i) {
