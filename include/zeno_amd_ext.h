@@ -168,6 +168,17 @@ int zeno_amd_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* 
 int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
                                     ZenoAmdContactResult* out);
 
+/* No counterpart in the reference. zeno_amd_detect_collisions_host for callers that cannot
+ * allocate device memory (serving loops and harnesses that forbid hipMalloc): the operands
+ * and results are staged in a static device array of ZENO_AMD_NOALLOC_MAX_PAIRS pairs
+ * (3 MiB on each GPU the library runs on, held until the process ends) instead of buffers
+ * allocated per call, and nothing is allocated or freed. n above that limit returns
+ * ZENO_INVALID_ARGUMENT. Runs on the current device and waits. Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (from several host threads) race. */
+#define ZENO_AMD_NOALLOC_MAX_PAIRS 16384u
+int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                            ZenoAmdContactResult* out);
+
 #ifdef __cplusplus
 }
 #endif

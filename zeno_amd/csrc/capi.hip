@@ -498,4 +498,16 @@ int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdColli
     return hip_status(e, "detect_collisions_host");
 }
 
+int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                            ZenoAmdContactResult* out) {
+    if (n == 0) return ZENO_SUCCESS;
+    if (!a || !b || !out) return ZENO_INVALID_ARGUMENT;
+    if (n > ZENO_AMD_NOALLOC_MAX_PAIRS) {
+        set_error("detect_collisions_host_noalloc: " + std::to_string(n) + " pairs exceed its static staging array of " +
+                  std::to_string(ZENO_AMD_NOALLOC_MAX_PAIRS) + " pairs (zeno_amd_detect_collisions_host takes any n)");
+        return ZENO_INVALID_ARGUMENT;
+    }
+    return hip_status(za::detect_collisions_host_noalloc(a, b, n, out), "detect_collisions_host_noalloc");
+}
+
 }  // extern "C"

@@ -11,4 +11,10 @@ namespace za {
 hipError_t launch_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n, ZenoAmdContactResult* out,
                                     hipStream_t stream);
 
+// The same on host arrays with no device allocation: operands and results are staged in the
+// library's static device array (at most ZENO_AMD_NOALLOC_MAX_PAIRS pairs, else
+// hipErrorInvalidValue). Blocking; calls that overlap on one GPU race for the array.
+hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                          ZenoAmdContactResult* out);
+
 }  // namespace za

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "collide.h"
 #include "narrow_ext.h"
 
@@ -113,7 +115,59 @@ __global__ __launch_bounds__(kCollideBlock) void detect_collisions_kernel(const 
     }
 }
 
+// Staging of zeno_amd_detect_collisions_host_noalloc: operands a, operands b and results of
+// up to ZENO_AMD_NOALLOC_MAX_PAIRS pairs (64 B each, 3 MiB in all). Every GPU the library runs
+// on holds its own copy until the process ends, and every call on that GPU shares it. In host
+// code `scratch` names a host-side stand-in: its device address on each GPU comes from
+// hipGetSymbolAddress (scratch_on_current_device) and only that address reaches a kernel or
+// a copy.
+constexpr size_t kNoAllocPairs = ZENO_AMD_NOALLOC_MAX_PAIRS;
+constexpr size_t kNoAllocBytes = kNoAllocPairs * (2 * sizeof(ZenoAmdCollider) + sizeof(ZenoAmdContactResult));
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, looked up once per device with that
+// device current.
+hipError_t scratch_on_current_device(unsigned char** out) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *out = static_cast<unsigned char*>(addr[dev]);
+    return hipSuccess;
+}
+
 }  // namespace
+
+hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
+                                          ZenoAmdContactResult* out) {
+    if (n == 0) return hipSuccess;
+    if (n > kNoAllocPairs) return hipErrorInvalidValue;
+    unsigned char* base = nullptr;
+    hipError_t e = scratch_on_current_device(&base);
+    if (e != hipSuccess) return e;
+    ZenoAmdCollider* da = reinterpret_cast<ZenoAmdCollider*>(base);
+    ZenoAmdCollider* db = da + kNoAllocPairs;
+    ZenoAmdContactResult* dout = reinterpret_cast<ZenoAmdContactResult*>(db + kNoAllocPairs);
+    const size_t in_bytes = (size_t)n * sizeof(ZenoAmdCollider), out_bytes = (size_t)n * sizeof(ZenoAmdContactResult);
+    // The null stream orders the copies and the kernel; the kernel writes every result of
+    // the n pairs, so nothing left in the array by an earlier call is read.
+    if ((e = hipMemcpy(da, a, in_bytes, hipMemcpyHostToDevice)) != hipSuccess) return e;
+    if ((e = hipMemcpy(db, b, in_bytes, hipMemcpyHostToDevice)) != hipSuccess) return e;
+    if ((e = launch_detect_collisions(da, db, n, dout, nullptr)) != hipSuccess) return e;
+    return hipMemcpy(out, dout, out_bytes, hipMemcpyDeviceToHost);
+}
 
 hipError_t launch_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n, ZenoAmdContactResult* out,
                                     hipStream_t stream) {
