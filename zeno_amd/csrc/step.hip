@@ -415,6 +415,25 @@ __device__ __forceinline__ void solve_slider(const float4* r, const Lds& s) {
     if (inv_mass_b > 0) s.quat[ib] = tof4(qb);
 }
 
+// Inclusive max-scan of v over segments of G lanes (sl = lane within the segment): DPP row
+// shifts when a segment lies inside one 16-lane row, LDS-backed shuffles otherwise.
+template <int G>
+__device__ __forceinline__ uint32_t seg_max_scan(uint32_t v, uint32_t sl) {
+    if constexpr (G <= 16) {
+        auto step = [&](uint32_t t, uint32_t d) { if (sl >= d) v = t > v ? t : v; };
+        if constexpr (G > 1) step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false), 1);  // row_shr:1
+        if constexpr (G > 2) step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false), 2);  // row_shr:2
+        if constexpr (G > 4) step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false), 4);  // row_shr:4
+        if constexpr (G > 8) step((uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false), 8);  // row_shr:8
+    } else {
+        for (uint32_t d = 1; d < (uint32_t)G; d <<= 1) {
+            const uint32_t t = __shfl_up(v, d, G);
+            if (sl >= d) v = t > v ? t : v;
+        }
+    }
+    return v;
+}
+
 // ---------------------------------------------------------------------------------------
 // solve_contacts, all_shaders.metal:1644-1793.
 // ---------------------------------------------------------------------------------------
@@ -707,8 +726,10 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
 // workgroup. GROUP: the narrow phase visits the slots grouped by geom-type pair (the
 // extended-contact mode, one environment per workgroup); a separate instance, so that the
 // other shapes' register allocation is not touched by it.
+// Two waves per SIMD at most 256 registers: the one-environment shapes hide their memory
+// latency with a second resident wave, and more than 256 registers would leave one.
 template <int EPW, int PL, bool HASH, bool GROUP>
-__global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
     constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
@@ -743,11 +764,67 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
     };
 
     // ---- Model records (one blob per scene) and the env's working set -> LDS -----------
+    // The environment's HBM reads are issued first and held in registers (up to kPreBodies
+    // bodies, kPreSlots contact slots and two lambdas and joint torques per lane, which covers
+    // every shape but the largest scenes), then the model records are copied (the same blob
+    // for every workgroup: L2 hits), and only then is anything written to LDS, so the reads
+    // of the different arrays overlap instead of waiting for one another. Entries beyond the
+    // prefetch counts are copied by the loops after.
+    // A contact slot's four quads, read ahead into registers.
+    struct Slot4 { float4 q0, q1, q2, q3; };
+    auto read_slot = [](const ContactRec* r) {
+        const float4* v = (const float4*)r;
+        return Slot4{v[0], v[1], v[2], v[3]};
+    };
+    auto write_slot = [](ContactRec* r, const Slot4& x) {
+        float4* v = (float4*)r;
+        v[0] = x.q0; v[1] = x.q1; v[2] = x.q2; v[3] = x.q3;
+    };
+    constexpr uint32_t kPreSlots = 4;  // slots per lane read ahead: 4 G, 64 at four envs per wave
+    uint32_t count = 0, pcount = 0;
+    bool detached = false;
+    // The lane's first action (read by stage A of every substep) is loaded with the state.
+    const float act0 = (live && (uint32_t)sl < a.A) ? a.actions[(size_t)env * a.A + sl] : 0.0f;
+    const size_t eb = (size_t)env * B;
+    const ContactRec* gc = a.contacts + (size_t)env * M;
+    const uint32_t b0 = sl, j0 = sl;
+    float4 p_pos = make_float4(0, 0, 0, 0), p_quat = p_pos, p_vel = p_pos, p_ang = p_pos;
+    float p_jt = 0.0f, p_lam = 0.0f;
+    Slot4 c0{}, c1{}, c2{}, c3{};
+    if (live) {
+        if (b0 < B) {
+            p_pos = a.pos[eb + b0];
+            p_quat = a.quat[eb + b0];
+            p_vel = a.vel[eb + b0];
+            p_ang = a.angvel[eb + b0];
+        }
+        if (j0 < Jp) p_jt = a.jtrq[(size_t)env * Jp + j0];
+        if (j0 < N) p_lam = a.lam[(size_t)env * N + j0];
+        if (sl < M) c0 = read_slot(&gc[sl]);
+        if (sl + G < M) c1 = read_slot(&gc[sl + G]);
+        if (sl + 2 * G < M) c2 = read_slot(&gc[sl + 2 * G]);
+        if (sl + 3 * G < M) c3 = read_slot(&gc[sl + 3 * G]);
+        count = a.counts[env];
+        pcount = a.pcounts[env];
+        detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
+    }
     // With the model records in HBM, the working-set reads follow the copy of the solve
     // records and the geom staging without a barrier in between, so their HBM latencies
     // overlap.
     if (PL == PL_LDS) {
-        for (uint32_t i = tid; i < a.ml.bytes / 16u; i += kWave) ((uint4*)smem)[i] = a.model[i];
+        const uint32_t nq = a.ml.bytes / 16u;
+        uint4* const dst = (uint4*)smem;
+        for (uint32_t i0 = tid; i0 < nq; i0 += 4u * kWave) {
+            const uint32_t i1 = i0 + kWave, i2 = i0 + 2u * kWave, i3 = i0 + 3u * kWave;
+            const uint4 q0 = a.model[i0];
+            const uint4 q1 = i1 < nq ? a.model[i1] : q0;
+            const uint4 q2 = i2 < nq ? a.model[i2] : q0;
+            const uint4 q3 = i3 < nq ? a.model[i3] : q0;
+            dst[i0] = q0;
+            if (i1 < nq) dst[i1] = q1;
+            if (i2 < nq) dst[i2] = q2;
+            if (i3 < nq) dst[i3] = q3;
+        }
     } else {
         const uint4* src = a.model + a.ml.jrec / 16u;
         for (uint32_t i = tid; i < a.nrec * kJRecQuads; i += kWave) ((uint4*)s.jrec)[i] = src[i];
@@ -778,13 +855,15 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         fill_alpha();
     }
 
-    uint32_t count = 0, pcount = 0;
-    bool detached = false;
-    // The lane's first action (read by stage A of every substep) is loaded with the state.
-    const float act0 = (live && (uint32_t)sl < a.A) ? a.actions[(size_t)env * a.A + sl] : 0.0f;
     if (live) {
-        const size_t eb = (size_t)env * B;
-        for (uint32_t b = sl; b < B; b += G) {
+        if (b0 < B) {
+            s.pos[b0] = p_pos;
+            s.quat[b0] = p_quat;
+            s.vel[b0] = p_vel;
+            s.vb[b0] = p_vel;
+            s.angvel[b0] = p_ang;
+        }
+        for (uint32_t b = sl + G; b < B; b += G) {
             s.pos[b] = a.pos[eb + b];
             s.quat[b] = a.quat[eb + b];
             float4 v = a.vel[eb + b];
@@ -792,19 +871,19 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             s.vb[b] = v;
             s.angvel[b] = a.angvel[eb + b];
         }
-        for (uint32_t j = sl; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
-        for (uint32_t i = sl; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
-        const ContactRec* gc = a.contacts + (size_t)env * M;
+        if (j0 < Jp) s.jt[j0] = p_jt;
+        if (j0 < N) s.lam[j0] = p_lam;
+        for (uint32_t j = sl + G; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
+        for (uint32_t i = sl + G; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
+        if (sl < M) { write_slot(&s.con[sl], c0); s.perm[sl] = (uint16_t)sl; }
+        if (sl + G < M) { write_slot(&s.con[sl + G], c1); s.perm[sl + G] = (uint16_t)(sl + G); }
+        if (sl + 2 * G < M) { write_slot(&s.con[sl + 2 * G], c2); s.perm[sl + 2 * G] = (uint16_t)(sl + 2 * G); }
+        if (sl + 3 * G < M) { write_slot(&s.con[sl + 3 * G], c3); s.perm[sl + 3 * G] = (uint16_t)(sl + 3 * G); }
 #pragma unroll 4
-        for (uint32_t k = sl; k < M; k += G) {
-            const float4* src = (const float4*)&gc[k];
-            float4* dst = (float4*)&s.con[k];
-            dst[0] = src[0]; dst[1] = src[1]; dst[2] = src[2]; dst[3] = src[3];
+        for (uint32_t k = sl + kPreSlots * G; k < M; k += G) {
+            write_slot(&s.con[k], read_slot(&gc[k]));
             s.perm[k] = (uint16_t)k;
         }
-        count = a.counts[env];
-        pcount = a.pcounts[env];
-        detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
     }
     __syncthreads();
     if (PL != PL_LDS) fill_alpha();
@@ -822,7 +901,10 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                                         __uint_as_float(pair_key(r->indices[0], r->indices[1])));
             }
         }
-        // ---- A: warm_start_constraints + apply_actions (:1408-1426, :196-229) ---------
+        // ---- A + B: warm_start_constraints, apply_actions (:1408-1426, :196-229), then per
+        // body compute_forces and update_kinematic in dispatch order (:345-388, :304-339,
+        // world.zig:962-990: the torque reads the quaternion before a kinematic body's
+        // update) and save_prev_state (:1900-1913). Each lane touches only its own entries.
         if (live) {
             for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
             for (uint32_t k = sl; k < a.A; k += G) {
@@ -832,14 +914,9 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
                 s.jt[(uint32_t)act.params[0]] = torque;
             }
-        }
-        __syncthreads();
-        // ---- B: compute_forces, then update_kinematic (:345-388, :304-339) ----------
-        // In dispatch order (world.zig:962-990): the torque reads the quaternion before a
-        // kinematic body's update.
-        if (live) {
             for (uint32_t b = sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
+                float4 P = s.pos[b], Q = s.quat[b];
                 if (imi.x < 1e-8f) {
                     s.frc[b] = make_float4(0, 0, 0, 0);
                     s.trq[b] = make_float4(0, 0, 0, 0);
@@ -847,23 +924,26 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     float mass = 1.0f / imi.x;
                     f3 force = mk3(a.gx * mass, a.gy * mass, a.gz * mass);
                     s.frc[b] = tof4(force, 0.0f);
-                    f3 cw = qrot(xyz(md.com[b]), toq(s.quat[b]));
+                    f3 cw = qrot(xyz(md.com[b]), toq(Q));
                     s.trq[b] = tof4(cross(cw, force), 0.0f);
                 }
                 if (md.flags[b] & 1u) {
-                    f3 p = add(xyz(s.pos[b]), scale(xyz(s.vel[b]), a.dt));
-                    s.pos[b] = tof4(p, 0.0f);
-                    q4 q = toq(s.quat[b]);
+                    P = tof4(add(xyz(P), scale(xyz(s.vel[b]), a.dt)), 0.0f);
+                    const q4 q = toq(Q);
                     f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
-                    s.quat[b] = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
+                    Q = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
+                    s.pos[b] = P;
+                    s.quat[b] = Q;
                 }
+                s.ppos[b] = P;
+                s.pquat[b] = Q;
             }
         }
         __syncthreads();
-        // ---- C: apply_joint_forces (S2) + save_prev_state (:122-190, :1900-1913) ------
+        // ---- C: apply_joint_forces (S2, :122-190) -------------------------------------
         // Each joint's world-frame contribution axis_world * tau is formed by one lane into
         // jw (skipped when |tau| < 1e-6, flag w = 0); then each body sums the contributions
-        // of its joints in ascending joint order (build_body_joint_lists).
+        // of its joints in ascending joint order (build_body_joint_lists), and integrates.
         if (live) {
             for (uint32_t j = sl; j < a.J; j += G) {
                 const JointRec& jr = md.joints[j];
@@ -875,17 +955,15 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 }
                 s.jw[j] = c;
             }
-            for (uint32_t b = sl; b < B; b += G) {
-                s.ppos[b] = s.pos[b];
-                s.pquat[b] = s.quat[b];
-            }
         }
         __syncthreads();
+        // ---- D: integrate (:394-462), on the lane that formed the body's forces -----------
         if (live) {
             for (uint32_t b = sl; b < B; b += G) {
-                const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
-                if (e0 == e1) continue;
+                const float4 imi = md.invmi[b];
+                if (imi.x < 1e-8f) continue;
                 float4 f = s.frc[b], t = s.trq[b];
+                const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
                 for (uint32_t e = e0; e < e1; ++e) {
                     const uint32_t ent = md.bjl[e];
                     const float4 c = s.jw[ent & 0x3FFFFFFFu];
@@ -894,22 +972,12 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     if (ent & (1u << 31)) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
                     else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
                 }
-                s.frc[b] = f;
-                s.trq[b] = t;
-            }
-        }
-        __syncthreads();
-        // ---- D: integrate (:394-462) -------------------------------------------------
-        if (live) {
-            for (uint32_t b = sl; b < B; b += G) {
-                const float4 imi = md.invmi[b];
-                if (imi.x < 1e-8f) continue;
-                f3 vel = add(xyz(s.vel[b]), scale(scale(xyz(s.frc[b]), imi.x), a.dt));
+                f3 vel = add(xyz(s.vel[b]), scale(scale(xyz(f), imi.x), a.dt));
                 vel = scale(vel, 0.999f);
                 f3 pos = add(xyz(s.pos[b]), scale(vel, a.dt));
                 s.vel[b] = tof4(vel, 0.0f);
                 s.pos[b] = tof4(pos, 0.0f);
-                f3 om = add(xyz(s.angvel[b]), scale(mul(mk3(imi.y, imi.z, imi.w), xyz(s.trq[b])), a.dt));
+                f3 om = add(xyz(s.angvel[b]), scale(mul(mk3(imi.y, imi.z, imi.w), xyz(t)), a.dt));
                 om = scale(om, 0.999f);
                 q4 q = toq(s.quat[b]);
                 f3 h = scale(scale(om, a.dt), 0.5f);
@@ -1147,30 +1215,65 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         __syncthreads();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
         // The snapshot is key-sorted (it is a sorted list from the last substep), so the
-        // entries with this slot's body pair form one run: its first entry is found by binary
-        // search and the run is scanned in index order up to the first other key, which gives
-        // the reference's first strict minimum.
+        // entries with this slot's body pair form one run; the match is the run's first
+        // entry at the smallest squared distance below 0.04 (the reference's first strict
+        // minimum in index order). Each snapshot entry's run start comes from a segmented
+        // max-scan over the sorted keys (on the sort-key region, free from here to the
+        // levels). Once the list has stopped growing, snapshot entry k holds the same pair as
+        // slot k and the slot's run starts at entry k's; otherwise the run's first entry is
+        // found by binary search. The run is read four entries per LDS round trip.
+        const uint32_t pn = pcount < M ? pcount : M;
+        auto key_at = [&](uint32_t i) { return __float_as_uint(s.pimp[i].w); };
+        uint32_t* const rstart = s.skey;
         if (live) {
-            const uint32_t pn = pcount < M ? pcount : M;
+            uint32_t carry = 0;
+            for (uint32_t base = 0; base < pn; base += G) {
+                const uint32_t i = base + sl;
+                uint32_t v = 0;
+                if (i < pn && i > 0 && key_at(i - 1) != key_at(i)) v = i;
+                v = seg_max_scan<G>(v, sl);
+                v = carry > v ? carry : v;
+                if (i < pn) rstart[i] = v;
+                carry = __shfl(v, G - 1, G);
+            }
+        }
+        wave_sync<HBM>();
+        if (live) {
             for (uint32_t k = sl; k < n_live; k += G) {
                 ContactRec* c = &s.con[s.perm[k]];
                 if (c->position_pen[3] < 0) continue;
                 const uint32_t key = pair_key(c->indices[0], c->indices[1]);
-                uint32_t lo = 0, hi = pn;
-                while (lo < hi) {
-                    uint32_t mid = (lo + hi) >> 1;
-                    if (__float_as_uint(s.pimp[mid].w) < key) lo = mid + 1; else hi = mid;
+                uint32_t lo;
+                if (k < pn && key_at(k) == key) {
+                    lo = rstart[k];
+                } else {
+                    uint32_t hi = pn;
+                    lo = 0;
+                    while (lo < hi) {
+                        uint32_t mid = (lo + hi) >> 1;
+                        if (key_at(mid) < key) lo = mid + 1; else hi = mid;
+                    }
                 }
                 const f3 p = mk3(c->position_pen[0], c->position_pen[1], c->position_pen[2]);
                 float best = 0.04f;
                 int best_i = -1;
                 // The run ends at the first entry with another key (the list is sorted).
-                for (uint32_t i = lo; i < pn && __float_as_uint(s.pimp[i].w) == key; ++i) {
-                    const float4 q = s.ppen[i];
-                    if (q.w < 0) continue;
-                    f3 d = sub(mk3(q.x, q.y, q.z), p);
-                    float dsq = dot(d, d);
-                    if (dsq < best) { best = dsq; best_i = (int)i; }
+                bool more = true;
+                auto visit = [&](uint32_t j, uint32_t kj, float4 q) {
+                    if (!(more && j < pn && kj == key)) { more = false; return; }
+                    if (q.w < 0) return;
+                    const f3 d = sub(mk3(q.x, q.y, q.z), p);
+                    const float dsq = dot(d, d);
+                    if (dsq < best) { best = dsq; best_i = (int)j; }
+                };
+                for (uint32_t i = lo; more && i < pn; i += 4) {
+                    const uint32_t j1 = i + 1 < pn ? i + 1 : i, j2 = i + 2 < pn ? i + 2 : i, j3 = i + 3 < pn ? i + 3 : i;
+                    const uint32_t k0 = key_at(i), k1 = key_at(j1), k2 = key_at(j2), k3 = key_at(j3);
+                    const float4 q0 = s.ppen[i], q1 = s.ppen[j1], q2 = s.ppen[j2], q3 = s.ppen[j3];
+                    visit(i, k0, q0);
+                    visit(i + 1, k1, q1);
+                    visit(i + 2, k2, q2);
+                    visit(i + 3, k3, q3);
                 }
                 if (best_i >= 0) {
                     const float4 im = s.pimp[best_i];
@@ -1183,24 +1286,28 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
         // ---- Contact levels for S4 -----------------------------------------------------
         // level(slot) = 1 + max level of earlier valid slots sharing a body that the solve
         // writes (inv_m > 1e-8). Running levels in order reproduces the sequential slot
-        // order exactly. Valid slots (solve_contacts skips only pen < 0, :1667) are
-        // compacted in slot order with a ballot, and each dynamic body gets a bit mask of
-        // the compacted slots touching it. Along one body the levels increase, so a slot's
-        // level is 1 + the larger level of its predecessors on its two bodies (the highest
-        // lower bit of each body's mask); levels follow by relaxation, one pass per level,
-        // and each level's slots are placed in slot order by a ballot into s.lst, level l
-        // owning [s.loff[l - 1], s.loff[l]).
+        // order exactly, and the slots of one level share no such body, so they may run in
+        // any order. Valid slots (solve_contacts skips only pen < 0, :1667) are compacted in
+        // slot order with a ballot, and each dynamic body gets a bit mask of the compacted
+        // slots touching it. When no slot of the environment writes two bodies (contacts
+        // with static geometry), a slot's level is its rank among the slots of its body: 1 +
+        // the number of lower bits in that body's mask. Otherwise a slot's level is 1 + the
+        // larger level of its predecessors on its two bodies (the highest lower bit of each
+        // body's mask), and levels follow by relaxation, one pass per level. Each level's
+        // slots are then placed by a counting sort into s.lst, level l owning
+        // [s.loff[l - 1], s.loff[l]).
         __syncthreads();  // matching has read the snapshot, which the level arrays reuse
         uint32_t nv = 0;
         const uint32_t mw = (M + 63u) >> 6;                                        // mask words per body
         uint32_t* const vbod = s.vbod;  // u32[M] dynamic bodies
-        uint32_t* const prv = s.prv;    // u32[M] predecessors
+        uint32_t* const prv = s.prv;    // u32[M] predecessors, then the level counters
         const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
         const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);
         if (live) {
             for (uint32_t i = sl; i < B * mw; i += G) s.bmask[i] = 0ull;
         }
         wave_sync<HBM>();
+        bool two_bodies = false;  // some valid slot of this lane writes both of its bodies
         if (live) {
             for (uint32_t base = 0; base < n_live; base += G) {
                 const uint32_t k = base + sl;
@@ -1221,11 +1328,26 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                     const unsigned long long bit = 1ull << (at & 63u);
                     if (A != 0xFFFFu) atomicOr(&s.bmask[A * mw + (at >> 6)], bit);
                     if (Bd != 0xFFFFu) atomicOr(&s.bmask[Bd * mw + (at >> 6)], bit);
+                    two_bodies = two_bodies || (A != 0xFFFFu && Bd != 0xFFFFu);
                 }
                 nv += (uint32_t)__popcll(ballot & group_mask);
             }
         }
+        const bool relax = (__ballot(two_bodies) & group_mask) != 0ull;  // per environment
         wave_sync<HBM>();
+        if (live && !relax) {
+            for (uint32_t i = sl; i < nv; i += G) {
+                const uint32_t bo = vbod[i];
+                const uint32_t body = (bo & 0xFFFFu) != 0xFFFFu ? (bo & 0xFFFFu) : (bo >> 16);
+                uint32_t lv = 1;
+                if (body != 0xFFFFu) {
+                    const unsigned long long* m = &s.bmask[body * mw];
+                    for (uint32_t w = 0; w < (i >> 6); ++w) lv += (uint32_t)__popcll(m[w]);
+                    lv += (uint32_t)__popcll(m[i >> 6] & ((1ull << (i & 63u)) - 1ull));
+                }
+                s.order[i] = (uint16_t)lv;
+            }
+        }
         // Predecessor on a body: the highest set bit below slot i in the body's mask.
         auto pred = [&](uint32_t body, uint32_t i) -> uint32_t {
             if (body == 0xFFFFu) return 0xFFFFu;
@@ -1236,28 +1358,31 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
             }
             return 0xFFFFu;
         };
-        if (live) {
-            for (uint32_t i = sl; i < nv; i += G) {
-                const uint32_t bo = vbod[i];
-                prv[i] = pred(bo & 0xFFFFu, i) | (pred(bo >> 16, i) << 16);
-                s.order[i] = 1;
-            }
-        }
-        wave_sync<HBM>();
-        for (;;) {
-            bool changed = false;
-            if (live) {
+        if (__ballot(live && relax) != 0ull) {
+            if (live && relax) {
                 for (uint32_t i = sl; i < nv; i += G) {
-                    const uint32_t pr = prv[i], pa = pr & 0xFFFFu, pb = pr >> 16;
-                    const uint32_t la = pa != 0xFFFFu ? s.order[pa] : 0u;
-                    const uint32_t lb = pb != 0xFFFFu ? s.order[pb] : 0u;
-                    const uint32_t lv = (la > lb ? la : lb) + 1u;
-                    if (lv != s.order[i]) { s.order[i] = (uint16_t)lv; changed = true; }
+                    const uint32_t bo = vbod[i];
+                    prv[i] = pred(bo & 0xFFFFu, i) | (pred(bo >> 16, i) << 16);
+                    s.order[i] = 1;
                 }
             }
             wave_sync<HBM>();
-            if (__ballot(changed) == 0ull) break;
+            for (;;) {
+                bool changed = false;
+                if (live && relax) {
+                    for (uint32_t i = sl; i < nv; i += G) {
+                        const uint32_t pr = prv[i], pa = pr & 0xFFFFu, pb = pr >> 16;
+                        const uint32_t la = pa != 0xFFFFu ? s.order[pa] : 0u;
+                        const uint32_t lb = pb != 0xFFFFu ? s.order[pb] : 0u;
+                        const uint32_t lv = (la > lb ? la : lb) + 1u;
+                        if (lv != s.order[i]) { s.order[i] = (uint16_t)lv; changed = true; }
+                    }
+                }
+                wave_sync<HBM>();
+                if (__ballot(changed) == 0ull) break;
+            }
         }
+        wave_sync<HBM>();
         {
             uint32_t nlev = 0;
             if (live) {
@@ -1267,25 +1392,46 @@ __global__ __launch_bounds__(kWave) void step_kernel(StepArgs a) {
                 const uint32_t t = __shfl_xor(nlev, d, G);
                 nlev = t > nlev ? t : nlev;
             }
-            uint32_t wave_nlev = nlev;  // the loop below runs to the largest count of the wave
+            uint32_t wave_nlev = nlev;  // the scan below runs to the largest count of the wave
             for (uint32_t d = G; d < 64u; d <<= 1) {
                 const uint32_t t = __shfl_xor(wave_nlev, d);
                 wave_nlev = t > wave_nlev ? t : wave_nlev;
             }
-            uint32_t run = 0;
-            if (live && sl == 0) s.loff[0] = 0;
-            for (uint32_t l = 1; l <= wave_nlev; ++l) {
-                for (uint32_t base = 0; base < M; base += G) {
-                    if (__ballot(live && base < nv) == 0ull) break;
-                    const uint32_t i = base + sl;
-                    const bool at_l = live && i < nv && s.order[i] == l;
-                    const uint64_t ballot = __ballot(at_l);
-                    if (at_l) s.lst[run + (uint32_t)__popcll(ballot & below)] = s.vlist[i];
-                    run += (uint32_t)__popcll(ballot & group_mask);
-                }
-                if (live && sl == 0 && l <= nlev) s.loff[l] = (uint16_t)run;
+            // Counting sort by level: per-level counts, their running sum (s.loff), then each
+            // slot takes the next place of its level.
+            uint32_t* const cnt = prv;  // u32[nlev]: entry l - 1 for level l (prv is dead now)
+            if (live) {
+                for (uint32_t l = sl; l < nlev; l += G) cnt[l] = 0u;
             }
-            if (live && sl == 0) s.misc[2] = nlev;
+            wave_sync<HBM>();
+            if (live) {
+                for (uint32_t i = sl; i < nv; i += G) atomicAdd(&cnt[s.order[i] - 1u], 1u);
+            }
+            wave_sync<HBM>();
+            uint32_t run = 0;
+            for (uint32_t l0 = 1; l0 <= wave_nlev; l0 += G) {
+                const uint32_t l = l0 + sl;
+                const bool mine = live && l <= nlev;
+                const uint32_t v = mine ? cnt[l - 1u] : 0u;
+                uint32_t incl = v;
+                for (uint32_t d = 1; d < (uint32_t)G; d <<= 1) {
+                    const uint32_t t = __shfl_up(incl, d, G);
+                    if ((uint32_t)sl >= d) incl += t;
+                }
+                if (mine) {
+                    s.loff[l] = (uint16_t)(run + incl);
+                    cnt[l - 1u] = run + incl - v;  // the level's first place
+                }
+                run += __shfl(incl, G - 1, G);
+            }
+            if (live && sl == 0) {
+                s.loff[0] = 0;
+                s.misc[2] = nlev;
+            }
+            wave_sync<HBM>();
+            if (live) {
+                for (uint32_t i = sl; i < nv; i += G) s.lst[atomicAdd(&cnt[s.order[i] - 1u], 1u)] = s.vlist[i];
+            }
         }
         // Per-slot constants of the contact solve (the same in every iteration): the bias
         // velocity, the two position-correction shares and the summed inverse mass, kept in
