@@ -48,10 +48,11 @@ def test_mode_is_off_by_default_and_switchable():
 
 
 def test_contact_list_beyond_lds_is_rejected():
-    """pile_hash (601 bodies) at max_contacts_per_env=1024 needs ~181 KB of LDS per
-    environment even with the working set in HBM: world creation fails with the sizes."""
+    """pile_hash (601 bodies) at max_contacts_per_env=2048 needs more LDS per environment than
+    a workgroup has even with the working set and the slot masks in HBM (the contact records
+    alone are 128 KB): world creation fails with the sizes."""
     with pytest.raises(RuntimeError, match="LDS working set"):
-        make_pair("pile_hash", 2, 1, max_contacts=1024)
+        make_pair("pile_hash", 2, 1, max_contacts=2048)
     # the failed shape queries leave no error behind for the next world
     g, o, acts = make_pair("pile", 2, 1, seed=7)
     g.step(acts[0])

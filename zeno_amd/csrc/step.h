@@ -47,6 +47,10 @@ inline uint32_t align16(uint32_t x) { return (x + 15u) & ~15u; }
 
 // Spatial-hash sort length: G rounded up to a power of two.
 inline uint32_t hash_pad(uint32_t G) { uint32_t p = 1; while (p < G) p <<= 1; return p; }
+// Contact lists longer than kRankSortMax slots per lane are sorted by a bitonic network over
+// the slots' keys (on skey) and logical positions (on order), both padded to a power of two.
+constexpr uint32_t kRankSortMax = 8;
+inline uint32_t sort_pad(uint32_t M) { return hash_pad(M); }
 // Spatial-hash scratch (on the sort-key region): hkey u32[Gp], hcell u32[G], then 16-B
 // aligned hpos float4[G] (world centre, radius) and hmeta uint4[G] (body, type, contype
 // mask, conaffinity group) of every geom, staged once per substep for the queries.
@@ -74,9 +78,9 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.lam = take(4 * (N > 0 ? N : 1));
     L.con = take(64 * M);
     L.perm = take(2 * M);
-    L.skey = take(std::max(std::max(4 * M, 16 * Jp), hash_bytes));  // also stage-C joint contributions, hash
+    L.skey = take(std::max(std::max(4 * sort_pad(M), 16 * Jp), hash_bytes));  // also stage-C joint contributions, hash
     L.ppen = take(16 * M); L.pimp = take(16 * M);
-    L.order = take(2 * M);
+    L.order = take(2 * sort_pad(M));
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
     L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
@@ -97,25 +101,29 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
 // With the working sets in HBM (placement 2) the arrays that the contact pipeline and the
 // spatial hash touch most (contact records, permutation, sort keys and everything aliased on
 // them, the snapshot, levels, body slot masks) still live in LDS, in this compact layout of
-// their own; only their offsets in the returned EnvLds are meaningful.
-inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0, bool stage_geoms = false) {
+// their own; only their offsets in the returned EnvLds are meaningful. With masks_in_lds
+// false the body slot masks stay in the HBM working set (bmask = kInHbm): scenes with many
+// bodies and long contact lists, whose masks alone would not fit.
+constexpr uint32_t kInHbm = 0xFFFFFFFFu;
+inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0, bool stage_geoms = false,
+                                 bool masks_in_lds = true) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
     const uint32_t hash_bytes = hash_bytes_for(G, true);
     L.con = take(64 * M);
     L.perm = take(2 * M);
-    const uint32_t mask_bytes = 8 * ((M + 63) / 64) * B;
+    const uint32_t mask_bytes = masks_in_lds ? 8 * ((M + 63) / 64) * B : 0u;
     // bmask follows vlist and lst on the sort-key region: the levels run after the sort and
     // the broad phase are done with it.
-    L.skey = take(std::max(std::max(4 * M + mask_bytes, 16 * Jp), hash_bytes));
+    L.skey = take(std::max(std::max(std::max(4 * M + mask_bytes, 4 * sort_pad(M)), 16 * Jp), hash_bytes));
     L.ppen = take(16 * M); L.pimp = take(16 * M);
-    L.order = take(2 * M);
+    L.order = take(2 * sort_pad(M));
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;
     L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
     L.hpos = L.skey + (G > kHashMinGeoms ? hash_hpos_off(G) : 0);
-    L.bmask = L.skey + 4 * M;
+    L.bmask = masks_in_lds ? L.skey + 4 * M : kInHbm;
     if (stage_geoms) { L.gst = take(16 * G); L.gmeta = take(4 * G); }
     L.misc = take(16);
     L.bytes = o;
@@ -351,8 +359,5 @@ int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t
 // 1 unless a.placement is PL_LDS and the hash is off.
 hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream);
 
-// Largest M supported for a given envs_per_wave (the sort and the contact schedule keep
-// M / lanes slots per lane in registers).
-inline uint32_t max_contacts_for(int envs_per_wave) { return 8u * (64u / (uint32_t)envs_per_wave); }
 
 }  // namespace za

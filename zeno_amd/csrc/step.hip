@@ -26,7 +26,7 @@ namespace za {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kMaxRecsPerLane = 8;
+constexpr int kMaxRecsPerLane = (int)kRankSortMax;
 
 __device__ __forceinline__ uint32_t pair_key(uint32_t a, uint32_t b) {
     uint32_t lo = a < b ? a : b, hi = a < b ? b : a;
@@ -99,7 +99,7 @@ __device__ __forceinline__ void bind_small(Lds& s, unsigned char* base, const En
     s.hkey = (uint32_t*)(base + L.hkey);
     s.hcell = (uint32_t*)(base + L.hcell);
     s.hpos = (float4*)(base + L.hpos);
-    s.bmask = (unsigned long long*)(base + L.bmask);
+    if (L.bmask != kInHbm) s.bmask = (unsigned long long*)(base + L.bmask);  // else: in the HBM working set
     s.gst = (float4*)(base + L.gst);
     s.gmeta = (uint32_t*)(base + L.gmeta);
     s.misc = (uint32_t*)(base + L.misc);
@@ -1119,40 +1119,95 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
         }
         __syncthreads();
         // ---- E.5: sort_contacts (:711-745), stable rank sort over the permutation ------
+        // Up to kMaxRecsPerLane slots per lane: each slot's rank (keys below it, plus equal
+        // keys at lower slots) is counted in registers. Longer lists: a bitonic network over
+        // (key, logical slot) pairs, keys on s.skey and slots on s.order padded to a power of
+        // two; the slot breaks ties between equal keys, so the order is the stable one.
         {
             const uint32_t n = count < M ? count : M;
             const bool need = live && count_before < M && count > count_before && n > 1;
-            if (need) {
-                for (uint32_t k = sl; k < n; k += G) {
-                    const uint32_t* idx = s.con[s.perm[k]].indices;
-                    s.skey[k] = pair_key(idx[0], idx[1]);
-                }
-            }
-            __syncthreads();
-            uint16_t keep[kMaxRecsPerLane];
-            uint32_t dst[kMaxRecsPerLane];
-            if (need) {
-#pragma unroll
-                for (int r = 0; r < kMaxRecsPerLane; ++r) {
-                    const uint32_t k = sl + r * G;
-                    if (k < n) {
-                        const uint32_t key = s.skey[k];
-                        uint32_t rank = 0;
-                        for (uint32_t j = 0; j < n; ++j) {
-                            const uint32_t kj = s.skey[j];
-                            rank += (kj < key || (kj == key && j < k)) ? 1u : 0u;
-                        }
-                        keep[r] = s.perm[k];
-                        dst[r] = rank;
+            const bool big = __ballot(need && n > (uint32_t)(kMaxRecsPerLane * G)) != 0ull;
+            if (!big) {
+                if (need) {
+                    for (uint32_t k = sl; k < n; k += G) {
+                        const uint32_t* idx = s.con[s.perm[k]].indices;
+                        s.skey[k] = pair_key(idx[0], idx[1]);
                     }
                 }
-            }
-            __syncthreads();
-            if (need) {
+                __syncthreads();
+                uint16_t keep[kMaxRecsPerLane];
+                uint32_t dst[kMaxRecsPerLane];
+                if (need) {
 #pragma unroll
-                for (int r = 0; r < kMaxRecsPerLane; ++r) {
-                    const uint32_t k = sl + r * G;
-                    if (k < n) s.perm[dst[r]] = keep[r];
+                    for (int r = 0; r < kMaxRecsPerLane; ++r) {
+                        const uint32_t k = sl + r * G;
+                        if (k < n) {
+                            const uint32_t key = s.skey[k];
+                            uint32_t rank = 0;
+                            for (uint32_t j = 0; j < n; ++j) {
+                                const uint32_t kj = s.skey[j];
+                                rank += (kj < key || (kj == key && j < k)) ? 1u : 0u;
+                            }
+                            keep[r] = s.perm[k];
+                            dst[r] = rank;
+                        }
+                    }
+                }
+                __syncthreads();
+                if (need) {
+#pragma unroll
+                    for (int r = 0; r < kMaxRecsPerLane; ++r) {
+                        const uint32_t k = sl + r * G;
+                        if (k < n) s.perm[dst[r]] = keep[r];
+                    }
+                }
+            } else {
+                // One environment per wave here (the long lists need EPW 1 or 2 to fit LDS);
+                // the network runs to the wave's largest padded length.
+                uint32_t np = 1;
+                while (np < n) np <<= 1;
+                uint32_t wave_np = need ? np : 1u;
+                for (uint32_t d = 1; d < 64u; d <<= 1) {
+                    const uint32_t t = __shfl_xor(wave_np, d);
+                    wave_np = t > wave_np ? t : wave_np;
+                }
+                if (need) {
+                    for (uint32_t k = sl; k < np; k += G) {
+                        uint32_t key = 0xFFFFFFFFu;
+                        if (k < n) {
+                            const uint32_t* idx = s.con[s.perm[k]].indices;
+                            key = pair_key(idx[0], idx[1]);
+                        }
+                        s.skey[k] = key;
+                        s.order[k] = (uint16_t)k;
+                    }
+                }
+                __syncthreads();
+                for (uint32_t kk = 2; kk <= wave_np; kk <<= 1) {
+                    for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
+                        if (need && kk <= np) {
+                            for (uint32_t t = sl; t < np / 2; t += G) {
+                                const uint32_t i = ((t & ~(j - 1u)) << 1) | (t & (j - 1u));
+                                const uint32_t l = i | j;
+                                const uint32_t xa = s.skey[i], xb = s.skey[l];
+                                const uint32_t ia = s.order[i], ib = s.order[l];
+                                const bool gt = xa > xb || (xa == xb && ia > ib);
+                                if (gt == ((i & kk) == 0)) {
+                                    s.skey[i] = xb; s.skey[l] = xa;
+                                    s.order[i] = (uint16_t)ib; s.order[l] = (uint16_t)ia;
+                                }
+                            }
+                        }
+                        __syncthreads();
+                    }
+                }
+                // order[k] = logical slot now at position k -> its physical slot, then perm.
+                if (need) {
+                    for (uint32_t k = sl; k < n; k += G) s.order[k] = s.perm[s.order[k]];
+                }
+                __syncthreads();
+                if (need) {
+                    for (uint32_t k = sl; k < n; k += G) s.perm[k] = s.order[k];
                 }
             }
         }

@@ -181,7 +181,10 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
-    const EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash);
+    // Placement 2 keeps the body slot masks in LDS when they fit, else in the HBM working set.
+    EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash, true);
+    if ((size_t)L_small.bytes > lds_max)
+        L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash, false);
     const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec,
                                       !w->hash, w->obsp);
     struct Cand { uint32_t pl; int epw; size_t shmem; };
@@ -193,14 +196,14 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     {
         std::vector<int> order;
         for (int cand : {8, 4, 2}) {
-            if (w->hash || w->M > max_contacts_for(cand)) continue;
+            if (w->hash) continue;
             if ((size_t)ML.bytes + (size_t)L.bytes * cand > 64 * 1024) continue;
             if ((w->E + cand - 1) / cand < 1024) continue;
             order.push_back(cand);
             break;
         }
         for (int cand : {1, 2, 4, 8}) {
-            if (cand > 1 && (w->hash || w->M > max_contacts_for(cand))) continue;
+            if (cand > 1 && w->hash) continue;
             if (std::find(order.begin(), order.end(), cand) == order.end()) order.push_back(cand);
         }
         for (int cand : order) {
@@ -231,7 +234,6 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->placement = best->pl;
     const int epw = best->epw;
     if (best->pl != PL_LDS) L = L_own;
-    if (w->M > max_contacts_for(epw)) { err = "max_contacts_per_env too large for this scene"; delete w; return nullptr; }
     w->lds = L;
     w->lds_small = L_small;
     w->epw = epw;
