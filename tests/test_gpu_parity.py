@@ -61,6 +61,19 @@ def test_launch_shapes_agree(epw):
     compare(gpu_arrays(g), oracle_arrays(o), **ONE_STEP)
 
 
+@pytest.mark.parametrize("name,envs,epw,waves", [("ant", 37, 4, 4), ("ant", 20, 2, 2), ("humanoid", 21, 4, 4),
+                                                ("pendulum", 9, 1, 4)])
+def test_multi_wave_workgroups_agree(name, envs, epw, waves):
+    """Workgroups of several waves sharing one copy of the model records: each wave steps its
+    own environments; env counts that leave the last workgroup partly empty included."""
+    g, o, acts = make_pair(name, envs, 6, seed=17, envs_per_wave=epw, waves=waves)
+    assert g.launch_config()[0] == epw and g.waves_per_group() == waves
+    for k in range(6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), **ONE_STEP)
+
+
 def test_substeps_parity():
     g, o, acts = make_pair("cartpole", 16, 5, seed=13, substeps=3)
     for k in range(5):

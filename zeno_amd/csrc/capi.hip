@@ -420,10 +420,12 @@ int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave,
     if (envs_per_wave) *envs_per_wave = (uint32_t)w->epw;
     if (lds_bytes) {
         *lds_bytes = w->placement == za::PL_ALL_HBM ? w->lds_small.bytes
-                   : w->lds.bytes * (uint32_t)w->epw + (w->placement == za::PL_LDS ? w->ml.bytes : 0u);
+                   : w->lds.bytes * (uint32_t)(w->epw * w->waves) + (w->placement == za::PL_LDS ? w->ml.bytes : 0u);
     }
     return ZENO_SUCCESS;
 }
+
+uint32_t zeno_amd_world_waves_per_group(ZenoWorldHandle world) { return world ? (uint32_t)W(world)->waves : 0u; }
 
 int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash) {
     if (!world) return ZENO_INVALID_HANDLE;

@@ -26,6 +26,7 @@ namespace za {
 namespace {
 
 constexpr int kWave = 64;
+constexpr int kMaxWaves = 4;  // waves per workgroup (model records in LDS: one copy shared by all)
 constexpr int kMaxRecsPerLane = (int)kRankSortMax;
 
 __device__ __forceinline__ uint32_t pair_key(uint32_t a, uint32_t b) {
@@ -719,30 +720,38 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
 }
 
 // PL: where the model records and the working sets live (Placement): PL_LDS, both in LDS
-// (EPW environments per workgroup); PL_MODEL_HBM, the model blob read in place from HBM
-// and one working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work).
+// (EPW environments per wave, and up to kMaxWaves independent waves per workgroup sharing one
+// copy of the model records); PL_MODEL_HBM, the model blob read in place from HBM and one
+// working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work).
 // HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms) instead of the
 // candidate pair list. Both non-LDS placements and the hash run one environment per
 // workgroup. GROUP: the narrow phase visits the slots grouped by geom-type pair (the
 // extended-contact mode, one environment per workgroup); a separate instance, so that the
 // other shapes' register allocation is not touched by it.
+// The waves of a workgroup meet at one barrier, after the model records are in LDS; from
+// there each wave steps its own environments and synchronises with itself only.
 // Two waves per SIMD at most 256 registers: the one-environment shapes hide their memory
 // latency with a second resident wave, and more than 256 registers would leave one.
 template <int EPW, int PL, bool HASH, bool GROUP>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void step_kernel(StepArgs a) {
+__global__ __launch_bounds__(PL == PL_LDS && !HASH ? kMaxWaves * kWave : kWave) __attribute__((amdgpu_waves_per_eu(2)))
+void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
     constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     static_assert(!GROUP || EPW == 1, "type-grouped narrow phase: one environment per workgroup");
     extern __shared__ __align__(16) unsigned char smem[];
-    const int tid = threadIdx.x;
+    const int tid = (int)(threadIdx.x & (kWave - 1));    // lane
+    constexpr bool MULTI = PL == PL_LDS && !HASH;          // several waves per workgroup possible
+    const uint32_t wv = MULTI ? threadIdx.x / kWave : 0u;  // wave in this workgroup
+    const uint32_t W = MULTI ? blockDim.x / kWave : 1u;    // waves in this workgroup
+    const uint32_t wave_id = blockIdx.x * W + wv;
     const int le = tid / G;
     const int sl = tid % G;
-    const uint32_t env = blockIdx.x * EPW + le;
+    const uint32_t env = wave_id * EPW + le;
     const bool live = env < a.E;
-    unsigned char* const env_base = HBM ? a.work + (size_t)blockIdx.x * a.lds.bytes
-                                        : smem + (PL == PL_LDS ? a.ml.bytes : 0u);
+    unsigned char* const env_base = HBM ? a.work + (size_t)wave_id * a.lds.bytes
+                                        : smem + (PL == PL_LDS ? a.ml.bytes : 0u) + wv * EPW * a.lds.bytes;
     Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
     if (HBM) bind_small(s, smem, a.lds_small);
     bind_levels(s, a.M);
@@ -752,7 +761,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
     const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
 
     // Phase timer: workgroup 0, lane 0 accumulates wall-clock ticks per phase.
-    const bool timer = a.phase_ticks != nullptr && blockIdx.x == 0 && tid == 0;
+    const bool timer = a.phase_ticks != nullptr && blockIdx.x == 0 && threadIdx.x == 0;
     unsigned long long t_last = timer ? (unsigned long long)wall_clock64() : 0ull;
     unsigned long long t_acc[kPhaseCount] = {};
     auto tick = [&](int ph) {
@@ -814,8 +823,9 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
     if (PL == PL_LDS) {
         const uint32_t nq = a.ml.bytes / 16u;
         uint4* const dst = (uint4*)smem;
-        for (uint32_t i0 = tid; i0 < nq; i0 += 4u * kWave) {
-            const uint32_t i1 = i0 + kWave, i2 = i0 + 2u * kWave, i3 = i0 + 3u * kWave;
+        const uint32_t nt = blockDim.x;
+        for (uint32_t i0 = threadIdx.x; i0 < nq; i0 += 4u * nt) {
+            const uint32_t i1 = i0 + nt, i2 = i0 + 2u * nt, i3 = i0 + 3u * nt;
             const uint4 q0 = a.model[i0];
             const uint4 q1 = i1 < nq ? a.model[i1] : q0;
             const uint4 q2 = i2 < nq ? a.model[i2] : q0;
@@ -839,8 +849,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
 
     // alpha~ = compliance / dt^2 (all_shaders.metal:928), the same value for every solve of
     // this launch: computed once per record, after the records have landed.
-    auto fill_alpha = [&]() {
-        for (uint32_t i = tid; i < a.nrec; i += kWave) {
+    auto fill_alpha = [&](uint32_t first, uint32_t stride) {
+        for (uint32_t i = first; i < a.nrec; i += stride) {
             float4* q = (float4*)md.jrec + i * kJRecQuads;
             if (joint_type_paired((fbits(q[0].w) >> 8) & 0xFFu)) {
                 q[2].w = q[2].w / (a.dt * a.dt);
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
     };
     if (PL == PL_LDS) {
         __syncthreads();
-        fill_alpha();
+        fill_alpha(threadIdx.x, blockDim.x);  // the workgroup's one copy of the records
     }
 
     if (live) {
@@ -885,8 +895,8 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
             s.perm[k] = (uint16_t)k;
         }
     }
-    __syncthreads();
-    if (PL != PL_LDS) fill_alpha();
+    __syncthreads();  // the last barrier of the workgroup: below, each wave syncs with itself
+    if (PL != PL_LDS) fill_alpha(tid, kWave);
     tick(PH_LOAD);
 
     for (uint32_t step = 0; step < a.substeps; ++step) {
@@ -939,7 +949,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 s.pquat[b] = Q;
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- C: apply_joint_forces (S2, :122-190) -------------------------------------
         // Each joint's world-frame contribution axis_world * tau is formed by one lane into
         // jw (skipped when |tau| < 1e-6, flag w = 0); then each body sums the contributions
@@ -956,7 +966,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 s.jw[j] = c;
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- D: integrate (:394-462), on the lane that formed the body's forces -----------
         if (live) {
             for (uint32_t b = sl; b < B; b += G) {
@@ -987,7 +997,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 s.quat[b] = tof4(q);
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         tick(PH_FORCES);
         // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
         const uint32_t count_before = count;
@@ -1013,7 +1023,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                     s.hkey[g] = key;
                 }
             }
-            __syncthreads();
+            wave_sync<HBM>();
             // Bitonic sort of the Gp keys: one compare-exchange pair per lane and pass.
             for (uint32_t k = 2; k <= a.Gp; k <<= 1) {
                 for (uint32_t j = k >> 1; j > 0; j >>= 1) {
@@ -1025,7 +1035,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                             if ((x > y) == ((i & k) == 0)) { s.hkey[i] = y; s.hkey[l] = x; }
                         }
                     }
-                    __syncthreads();
+                    wave_sync<HBM>();
                 }
             }
             // Queries (broad_phase_detect, :632-700): count each geom's pairs, place them
@@ -1117,7 +1127,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 count += total;
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- E.5: sort_contacts (:711-745), stable rank sort over the permutation ------
         // Up to kMaxRecsPerLane slots per lane: each slot's rank (keys below it, plus equal
         // keys at lower slots) is counted in registers. Longer lists: a bitonic network over
@@ -1134,7 +1144,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                         s.skey[k] = pair_key(idx[0], idx[1]);
                     }
                 }
-                __syncthreads();
+                wave_sync<HBM>();
                 uint16_t keep[kMaxRecsPerLane];
                 uint32_t dst[kMaxRecsPerLane];
                 if (need) {
@@ -1153,7 +1163,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                         }
                     }
                 }
-                __syncthreads();
+                wave_sync<HBM>();
                 if (need) {
 #pragma unroll
                     for (int r = 0; r < kMaxRecsPerLane; ++r) {
@@ -1182,7 +1192,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                         s.order[k] = (uint16_t)k;
                     }
                 }
-                __syncthreads();
+                wave_sync<HBM>();
                 for (uint32_t kk = 2; kk <= wave_np; kk <<= 1) {
                     for (uint32_t j = kk >> 1; j > 0; j >>= 1) {
                         if (need && kk <= np) {
@@ -1198,20 +1208,20 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                                 }
                             }
                         }
-                        __syncthreads();
+                        wave_sync<HBM>();
                     }
                 }
                 // order[k] = logical slot now at position k -> its physical slot, then perm.
                 if (need) {
                     for (uint32_t k = sl; k < n; k += G) s.order[k] = s.perm[s.order[k]];
                 }
-                __syncthreads();
+                wave_sync<HBM>();
                 if (need) {
                     for (uint32_t k = sl; k < n; k += G) s.perm[k] = s.order[k];
                 }
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         tick(PH_BROAD);
         // ---- F: narrow_phase (:751-894) -----------------------------------------------
         const uint32_t n_live = count < M ? count : M;
@@ -1233,11 +1243,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
             };
             constexpr uint32_t kPer = 64u / G;  // classes per lane
             for (uint32_t i = 0; i < kPer; ++i) ccount[sl * kPer + i] = 0u;
-            __syncthreads();
+            wave_sync<HBM>();
             if (live) {
                 for (uint32_t k = sl; k < n_live; k += G) atomicAdd(&ccount[slot_class(s.perm[k])], 1u);
             }
-            __syncthreads();
+            wave_sync<HBM>();
             // Exclusive scan of the env's 64 counters: each lane sums its kPer classes, the
             // env's G lanes scan those sums, and each lane writes its classes' offsets.
             uint32_t sum = 0;
@@ -1253,21 +1263,21 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 ccount[sl * kPer + i] = run;
                 run += c;
             }
-            __syncthreads();
+            wave_sync<HBM>();
             if (live) {
                 for (uint32_t k = sl; k < n_live; k += G) {
                     const uint32_t phys = s.perm[k];
                     s.order[atomicAdd(&ccount[slot_class(phys)], 1u)] = (uint16_t)phys;
                 }
             }
-            __syncthreads();
+            wave_sync<HBM>();
             if (live) {
                 for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.order[k]]);
             }
         } else if (live) {
             for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.perm[k]]);
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
         // The snapshot is key-sorted (it is a sorted list from the last substep), so the
         // entries with this slot's body pair form one run; the match is the run's first
@@ -1351,7 +1361,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
         // body's mask), and levels follow by relaxation, one pass per level. Each level's
         // slots are then placed by a counting sort into s.lst, level l owning
         // [s.loff[l - 1], s.loff[l]).
-        __syncthreads();  // matching has read the snapshot, which the level arrays reuse
+        wave_sync<HBM>();  // matching has read the snapshot, which the level arrays reuse
         uint32_t nv = 0;
         const uint32_t mw = (M + 63u) >> 6;                                        // mask words per body
         uint32_t* const vbod = s.vbod;  // u32[M] dynamic bodies
@@ -1503,11 +1513,11 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                                            pos_correction * (inv_mass_b / inv_mass_sum), inv_mass_sum);
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         uint32_t max_lev = 0;
         for (int e2 = 0; e2 < EPW; ++e2) {
             const uint32_t* m2 = HBM ? s.misc : (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
-            if (blockIdx.x * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
+            if (wave_id * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
         }
         const uint32_t my_nlev = live ? s.misc[2] : 0u;
         tick(PH_NARROW);
@@ -1634,7 +1644,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 s.angvel[b] = tof4(scale(sscale(2.0f, xyz(dq)), inv_dt), 0.0f);
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- K: update_joint_states (:1550-1638) ------------------------------------
         if (live) {
             for (uint32_t j = sl; j < a.J; j += G) {
@@ -1662,7 +1672,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
                 s.jv[j] = jv;
             }
         }
-        __syncthreads();
+        wave_sync<HBM>();
         // ---- L: read_sensors (:1799-1893); cache_contacts is the next snapshot --------
         // The row is assembled in the working set and written back with the state. Entries
         // that no sensor writes are 0 (nothing else ever writes the observation buffer).
@@ -1691,7 +1701,7 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2))) void
             }
         }
         pcount = count;
-        __syncthreads();
+        wave_sync<HBM>();
         tick(PH_POST);
     }
 
@@ -1782,13 +1792,13 @@ hipError_t allow_lds(size_t shmem) {
 }
 
 template <int EPW, int PL, bool HASH, bool GROUP = false>
-int resident_as(size_t shmem) {
+int resident_as(size_t shmem, int waves = 1) {
     // A shape that does not fit is an answer here, not an error: the failed query's error
     // is taken off HIP's last-error slot so that later hipGetLastError checks (of this or
     // another world) do not report it.
     int n = 0;
     if (allow_lds<EPW, PL, HASH, GROUP>(shmem) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH, GROUP>, kWave, shmem) != hipSuccess) {
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH, GROUP>, kWave * waves, shmem) != hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
@@ -1796,9 +1806,9 @@ int resident_as(size_t shmem) {
 }
 
 template <int EPW, int PL, bool HASH, bool GROUP = false>
-hipError_t launch_as(const StepArgs& a, uint32_t blocks, size_t shmem, hipStream_t stream) {
+hipError_t launch_as(const StepArgs& a, uint32_t blocks, size_t shmem, hipStream_t stream, int waves = 1) {
     ZA_CHECK((allow_lds<EPW, PL, HASH, GROUP>(shmem)));
-    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH, GROUP>), dim3(blocks), dim3(kWave), shmem, stream, a);
+    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH, GROUP>), dim3(blocks), dim3(kWave * waves), shmem, stream, a);
     return hipGetLastError();
 }
 
@@ -1810,9 +1820,10 @@ size_t max_lds_per_workgroup(int device) {
     return (size_t)v;
 }
 
-int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem) {
+int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem, int waves) {
+    if (waves < 1 || waves > kMaxWaves) return 0;
     if (hash || placement != PL_LDS) {
-        if (envs_per_wave != 1) return 0;
+        if (envs_per_wave != 1 || waves != 1) return 0;
         switch (placement) {
             case PL_LDS: return resident_as<1, PL_LDS, true>(shmem);
             case PL_MODEL_HBM: return hash ? resident_as<1, PL_MODEL_HBM, true>(shmem) : resident_as<1, PL_MODEL_HBM, false>(shmem);
@@ -1821,21 +1832,23 @@ int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t
         }
     }
     switch (envs_per_wave) {
-        case 1: return resident_as<1, PL_LDS, false>(shmem);
-        case 2: return resident_as<2, PL_LDS, false>(shmem);
-        case 4: return resident_as<4, PL_LDS, false>(shmem);
-        case 8: return resident_as<8, PL_LDS, false>(shmem);
+        case 1: return resident_as<1, PL_LDS, false>(shmem, waves);
+        case 2: return resident_as<2, PL_LDS, false>(shmem, waves);
+        case 4: return resident_as<4, PL_LDS, false>(shmem, waves);
+        case 8: return resident_as<8, PL_LDS, false>(shmem, waves);
         default: return 0;
     }
 }
 
-hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream) {
+hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStream_t stream) {
     if (a.E == 0) return hipSuccess;
-    const uint32_t blocks = (a.E + (uint32_t)envs_per_wave - 1) / (uint32_t)envs_per_wave;
-    if ((a.placement != PL_LDS || a.hash) && envs_per_wave != 1) return hipErrorInvalidValue;
+    if (waves < 1 || waves > kMaxWaves) return hipErrorInvalidValue;
+    const uint32_t per_group = (uint32_t)envs_per_wave * (uint32_t)waves;
+    const uint32_t blocks = (a.E + per_group - 1) / per_group;
+    if ((a.placement != PL_LDS || a.hash) && (envs_per_wave != 1 || waves != 1)) return hipErrorInvalidValue;
     if ((a.placement == PL_ALL_HBM) != (a.work != nullptr)) return hipErrorInvalidValue;
     const size_t env_lds = (size_t)a.lds.bytes * (size_t)envs_per_wave;
-    const size_t shmem = (size_t)a.ml.bytes + env_lds;
+    const size_t shmem = (size_t)a.ml.bytes + env_lds * (size_t)waves;
     // Extended-contact mode with one environment per workgroup: the instance whose narrow
     // phase visits the slots grouped by geom-type pair (same results, less divergence).
     if (a.ext_contacts && a.M >= 64 && envs_per_wave == 1) {
@@ -1864,10 +1877,10 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, hipStream_t stream)
     }
     if (a.hash) return launch_as<1, PL_LDS, true>(a, blocks, shmem, stream);
     switch (envs_per_wave) {
-        case 1: return launch_as<1, PL_LDS, false>(a, blocks, shmem, stream);
-        case 2: return launch_as<2, PL_LDS, false>(a, blocks, shmem, stream);
-        case 4: return launch_as<4, PL_LDS, false>(a, blocks, shmem, stream);
-        case 8: return launch_as<8, PL_LDS, false>(a, blocks, shmem, stream);
+        case 1: return launch_as<1, PL_LDS, false>(a, blocks, shmem, stream, waves);
+        case 2: return launch_as<2, PL_LDS, false>(a, blocks, shmem, stream, waves);
+        case 4: return launch_as<4, PL_LDS, false>(a, blocks, shmem, stream, waves);
+        case 8: return launch_as<8, PL_LDS, false>(a, blocks, shmem, stream, waves);
         default: return hipErrorInvalidValue;
     }
 }

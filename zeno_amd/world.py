@@ -401,6 +401,11 @@ class ZenoWorld:
         self._lib.zeno_amd_world_launch_config(self._handle, C.byref(epw), C.byref(lds))
         return epw.value, lds.value
 
+    def waves_per_group(self) -> int:
+        """Waves per workgroup of the step launches (the waves of a workgroup share one copy
+        of the model records in LDS)."""
+        return int(self._lib.zeno_amd_world_waves_per_group(self._handle))
+
     def modes(self) -> Dict[str, Any]:
         """{"placement": 0 model + working sets in LDS, 1 model in HBM and working set in LDS,
         2 both in HBM; "spatial_hash": the spatial-hash broad phase runs (G > 512)}."""
