@@ -183,6 +183,13 @@ int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdColli
 int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
                                             ZenoAmdContactResult* out);
 
+/* No counterpart in the reference: a self-check of the device arithmetic the step relies on.
+ * q[i] = a[i] / b[i] evaluated the way the step kernel divides several numbers by one divisor
+ * (one fp64 reciprocal from v_rcp_f64 and two Newton steps, then fp32(a * y)), which must give
+ * the bits of the IEEE fp32 division for every input. Host arrays; runs on the current
+ * device and waits. */
+int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,20 @@ def test_multi_wave_workgroups_agree(name, envs, epw, waves):
         compare(gpu_arrays(g), oracle_arrays(o), **ONE_STEP)
 
 
+@pytest.mark.parametrize("waves", [2, 4])
+def test_grouped_narrow_phase_multi_wave(waves):
+    """Extended-contact mode at one environment per wave launches the narrow-phase instance
+    that visits slots grouped by geom-type pair; with several waves per workgroup every wave
+    steps its own environment (11 envs: the last workgroup partly empty)."""
+    g, o, acts = make_pair("ant", 11, 6, seed=19, envs_per_wave=1, waves=waves, extended_contacts=True)
+    assert g.launch_config()[0] == 1 and g.waves_per_group() == waves
+    for k in range(6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    assert np.all(g.get_contact_counts() > 0)
+
+
 def test_substeps_parity():
     g, o, acts = make_pair("cartpole", 16, 5, seed=13, substeps=3)
     for k in range(5):

@@ -512,4 +512,10 @@ int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const Zeno
     return hip_status(za::detect_collisions_host_noalloc(a, b, n, out), "detect_collisions_host_noalloc");
 }
 
+int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t n) {
+    if (n == 0) return ZENO_SUCCESS;
+    if (!a || !b || !q) return ZENO_INVALID_ARGUMENT;
+    return hip_status(za::selfcheck_divide_host(a, b, q, n), "selfcheck_divide");
+}
+
 }  // extern "C"

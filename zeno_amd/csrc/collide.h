@@ -17,4 +17,8 @@ hipError_t launch_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdColli
 hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
                                           ZenoAmdContactResult* out);
 
+// q[i] = a[i] / b[i] through the step kernel's shared-reciprocal division (dmath.h rcp64 and
+// div_r) on host arrays: copies in, runs on the current device, copies back, waits.
+hipError_t selfcheck_divide_host(const float* a, const float* b, float* q, uint32_t n);
+
 }  // namespace za

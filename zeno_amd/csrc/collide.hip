@@ -169,6 +169,33 @@ hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAm
     return hipMemcpy(out, dout, out_bytes, hipMemcpyDeviceToHost);
 }
 
+namespace {
+__global__ __launch_bounds__(256) void selfcheck_divide_kernel(const float* a, const float* b, float* q, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) q[i] = div_r(a[i], rcp64(b[i]));
+}
+}  // namespace
+
+hipError_t selfcheck_divide_host(const float* a, const float* b, float* q, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    const size_t bytes = (size_t)n * sizeof(float);
+    float *da = nullptr, *db = nullptr, *dq = nullptr;
+    hipError_t e = hipMalloc(&da, bytes);
+    if (e == hipSuccess) e = hipMalloc(&db, bytes);
+    if (e == hipSuccess) e = hipMalloc(&dq, bytes);
+    if (e == hipSuccess) e = hipMemcpy(da, a, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(db, b, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(selfcheck_divide_kernel, dim3((uint32_t)(((size_t)n + 255) / 256)), dim3(256), 0, nullptr, da, db, dq, n);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(q, dq, bytes, hipMemcpyDeviceToHost);
+    if (da) hipFree(da);
+    if (db) hipFree(db);
+    if (dq) hipFree(dq);
+    return e;
+}
+
 hipError_t launch_detect_collisions(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n, ZenoAmdContactResult* out,
                                     hipStream_t stream) {
     if (n == 0) return hipSuccess;

@@ -21,7 +21,28 @@ __device__ __forceinline__ f3 sub(f3 a, f3 b) { return {a.x - b.x, a.y - b.y, a.
 __device__ __forceinline__ f3 mul(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
 __device__ __forceinline__ f3 scale(f3 a, float s) { return {a.x * s, a.y * s, a.z * s}; }
 __device__ __forceinline__ f3 sscale(float s, f3 a) { return {s * a.x, s * a.y, s * a.z}; }
-__device__ __forceinline__ f3 divs(f3 a, float s) { return {a.x / s, a.y / s, a.z / s}; }
+// Several fp32 quotients with one divisor, through one fp64 reciprocal. For fp32 a and b the
+// exact quotient a / b is either an fp32 number or at least 2^-49 (relative) away from every
+// rounding boundary of the fp32 grid: with a = A 2^ea, b = B 2^eb (A, B < 2^24) and a boundary
+// m = M 2^em (M odd, < 2^25), a - m b is a nonzero multiple of 2^(em+eb), so
+// |a / b - m| >= 2^(em+eb) / b > 2^-49 m. y = 1 / b from v_rcp_f64 refined by two Newton steps
+// is within ~2^-53 (relative) of 1 / b; a * y rounded to fp64 is then within ~2^-52 of a / b, on
+// the same side of every boundary, so its rounding to fp32 is the correctly rounded a / b (the
+// bits of the fp32 division, subnormal and overflowing quotients included: the fp64 range holds
+// every fp32 quotient). A zero or infinite divisor keeps the raw reciprocal (+-inf, +-0, exact),
+// so a * y gives the IEEE quotient (+-inf, +-0 or NaN); a NaN divisor gives NaN.
+__device__ __forceinline__ double rcp64(float b) {
+    const double d = (double)b;
+    const double r0 = __builtin_amdgcn_rcp(d);
+    double r = __builtin_fma(r0, __builtin_fma(-d, r0, 1.0), r0);
+    r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
+    return (__builtin_isfinite(b) && b != 0.0f) ? r : r0;
+}
+__device__ __forceinline__ float div_r(float a, double y) { return (float)((double)a * y); }
+__device__ __forceinline__ f3 divs(f3 a, float s) {
+    const double y = rcp64(s);
+    return {div_r(a.x, y), div_r(a.y, y), div_r(a.z, y)};
+}
 __device__ __forceinline__ f3 neg(f3 a) { return {-a.x, -a.y, -a.z}; }
 __device__ __forceinline__ float dot(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 __device__ __forceinline__ float len(f3 a) { return __builtin_sqrtf(dot(a, a)); }
@@ -57,7 +78,9 @@ __device__ __forceinline__ f3 qrot(f3 v, q4 q) {
 __device__ __forceinline__ float qlen(q4 q) { return __builtin_sqrtf(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w); }
 __device__ __forceinline__ q4 qnormalize(q4 q) {
     const float l = qlen(q);
-    return l > 1e-8f ? q4{q.x / l, q.y / l, q.z / l, q.w / l} : q4{0.0f, 0.0f, 0.0f, 1.0f};
+    if (!(l > 1e-8f)) return q4{0.0f, 0.0f, 0.0f, 1.0f};
+    const double y = rcp64(l);  // q / l with one reciprocal (see divs)
+    return q4{div_r(q.x, y), div_r(q.y, y), div_r(q.z, y), div_r(q.w, y)};
 }
 // Quaternion step q + s * ((d, 0) (x) q) used by every XPBD rotation update.
 __device__ __forceinline__ q4 qdelta(f3 d, q4 q) { return qscale(qmul(mk4(d.x, d.y, d.z, 0.0f), q), 0.5f); }

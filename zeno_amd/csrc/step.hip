@@ -176,39 +176,51 @@ __device__ __forceinline__ void wave_sync() {
 // covers both bodies. Shared quantities (the constraint error, its direction, the
 // multiplier) are evaluated identically on both lanes, operands in the reference's order;
 // where the reference subtracts body b's update (x - d) the odd lane adds (-1 * d), which
-// is the same IEEE result.
-__device__ __forceinline__ float pair_swap(float v) {
-    // quad_perm(1, 0, 3, 2): exchange with the adjacent lane.
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+// is the same IEEE result. A sign applied to a product is applied to one of its factors
+// instead ((-1 * x) * y and x * (-1 * y) round identically), never to a sum, whose zero signs
+// it could change.
+template <int PERM>
+__device__ __forceinline__ float qperm(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), PERM, 0xF, 0xF, false));
 }
-__device__ __forceinline__ f3 pair_swap(f3 v) { return {pair_swap(v.x), pair_swap(v.y), pair_swap(v.z)}; }
-__device__ __forceinline__ q4 pair_swap(q4 v) { return {pair_swap(v.x), pair_swap(v.y), pair_swap(v.z), pair_swap(v.w)}; }
-__device__ __forceinline__ f3 sel(bool c, f3 x, f3 y) { return c ? x : y; }
-__device__ __forceinline__ q4 sel(bool c, q4 x, q4 y) { return c ? x : y; }
-__device__ __forceinline__ f3 signed3(float sg, f3 v) { return {sg * v.x, sg * v.y, sg * v.z}; }
-__device__ __forceinline__ q4 signed4(float sg, q4 v) { return {sg * v.x, sg * v.y, sg * v.z, sg * v.w}; }
+// quad_perm(1, 0, 3, 2): the partner lane's value.
+__device__ __forceinline__ float pair_swap(float v) { return qperm<0xB1>(v); }
+// quad_perm(0, 0, 2, 2) and (1, 1, 3, 3): the even (body a) and odd (body b) lane's value on
+// both lanes of the pair.
+__device__ __forceinline__ f3 pair_a(f3 v) { return {qperm<0xA0>(v.x), qperm<0xA0>(v.y), qperm<0xA0>(v.z)}; }
+__device__ __forceinline__ f3 pair_b(f3 v) { return {qperm<0xF5>(v.x), qperm<0xF5>(v.y), qperm<0xF5>(v.z)}; }
+__device__ __forceinline__ q4 pair_a(q4 v) { return {qperm<0xA0>(v.x), qperm<0xA0>(v.y), qperm<0xA0>(v.z), qperm<0xA0>(v.w)}; }
+__device__ __forceinline__ q4 pair_b(q4 v) { return {qperm<0xF5>(v.x), qperm<0xF5>(v.y), qperm<0xF5>(v.z), qperm<0xF5>(v.w)}; }
+// qdelta with its factor 0.5 carrying the lane's sign: sg * (0.5 * x) == (sg * 0.5) * x.
+__device__ __forceinline__ q4 qdelta_signed(f3 d, q4 q, float sg) { return qscale(qmul(mk4(d.x, d.y, d.z, 0.0f), q), 0.5f * sg); }
 
 // The lane's half of a lane-pair solve record (build_joint_program): header, the lane's
 // body's inverse mass and inertia, its vector (anchor or axis) with compliance / dt^2 in .w,
 // and its centre of mass or the angular limits.
 struct JHalf { float4 h0, mi, v1, v2; };
 __device__ __forceinline__ JHalf load_half(const float4* p) { return JHalf{p[0], p[1], p[2], p[3]}; }
+// The state a lane-pair solve reads for the lane's body: position, orientation and the
+// constraint's multiplier (every record's header holds a valid multiplier index).
+struct JState { float4 P, Q; float lam; };
+__device__ __forceinline__ JState load_jstate(const JHalf& h, const Lds& s, bool odd) {
+    const uint32_t me = odd ? fbits(h.h0.y) : fbits(h.h0.x);
+    return JState{s.pos[me], s.quat[me], s.lam[fbits(h.h0.z)]};
+}
 
 // :934-1037 positional (point-to-point), lane pair.
-__device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, bool odd) {
+__device__ __forceinline__ void solve_positional2(const JHalf& h, const JState& st, const Lds& s, bool odd) {
     const uint32_t ia = fbits(h.h0.x), ib = fbits(h.h0.y), ci = fbits(h.h0.z);
     const uint32_t me = odd ? ib : ia;
     const float alpha_tilde = h.v1.w;
     const float inv_mass = h.mi.x;
     const f3 iI = mk3(h.mi.y, h.mi.z, h.mi.w);
     const float sg = odd ? -1.0f : 1.0f;
-    const f3 P = xyz(s.pos[me]);
-    const q4 Q = toq(s.quat[me]);
-    const float lambda_prev = s.lam[ci];  // read with the body state: one LDS round trip
+    const f3 P = xyz(st.P);
+    const q4 Q = toq(st.Q);
+    const float lambda_prev = st.lam;
     const f3 rr = qrot(xyz(h.v1), Q);                      // r_a or r_b
     const f3 u = add(P, rr);                               // pos + r
-    const f3 uo = pair_swap(u);
-    const f3 diff = sub(sel(odd, uo, u), sel(odd, u, uo));  // (pos_a + r_a) - (pos_b + r_b)
+    const f3 diff = sub(pair_a(u), pair_b(u));             // (pos_a + r_a) - (pos_b + r_b)
     const float C = len(diff);
     if (C > 1e-6f) {
         const f3 n = divs(diff, C);
@@ -216,7 +228,7 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, 
         const float t = inv_mass + dot(mul(rn, iI), rn);
         const float w = t + pair_swap(t);                  // (w_a) + (w_b), addition commutes
         const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
-        if (!odd) s.lam[ci] = lambda_prev + d_lambda;
+        s.lam[ci] = lambda_prev + d_lambda;  // both lanes store the same value
         const f3 impulse = sscale(d_lambda, n);
         // r - qrot(com, q): with com = +0 and a finite q the rotated offset is exactly +0 and
         // r - (+0) = r, so the rotation is skipped. A finite sum of the components implies
@@ -227,22 +239,21 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const Lds& s, 
         f3 rc = rr;
         if (!com_zero) rc = sub(rr, qrot(xyz(h.v2), Q));
         if (inv_mass > 0) {
-            set_xyz(&s.pos[me], add(P, signed3(sg, scale(impulse, inv_mass))));
-            s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(cross(rc, impulse), iI), Q)))));
+            set_xyz(&s.pos[me], add(P, scale(impulse, sg * inv_mass)));
+            s.quat[me] = tof4(qnormalize(qadd(Q, qdelta_signed(mul(cross(rc, impulse), iI), Q, sg))));
         }
     }
 }
 
 // :1131-1186 hinge axis alignment, lane pair.
-__device__ __forceinline__ void solve_angular2(const JHalf& h, const Lds& s, bool odd) {
+__device__ __forceinline__ void solve_angular2(const JHalf& h, const JState& st, const Lds& s, bool odd) {
     const uint32_t me = odd ? fbits(h.h0.y) : fbits(h.h0.x);
     const float alpha_tilde = h.v1.w;
     const float inv_mass = h.mi.x;
     const f3 iI = mk3(h.mi.y, h.mi.z, h.mi.w);
-    const q4 Q = toq(s.quat[me]);
+    const q4 Q = toq(st.Q);
     const f3 axw = qrot(xyz(h.v1), Q);
-    const f3 axo = pair_swap(axw);
-    const f3 cr = cross(sel(odd, axo, axw), sel(odd, axw, axo));
+    const f3 cr = cross(pair_a(axw), pair_b(axw));
     const float sin_angle = len(cr);
     if (sin_angle > 1e-6f) {
         const f3 n = divs(cr, sin_angle);
@@ -258,7 +269,7 @@ __device__ __forceinline__ void solve_angular2(const JHalf& h, const Lds& s, boo
 }
 
 // :1189-1238 angular limit, lane pair.
-__device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const Lds& s, bool odd) {
+__device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const JState& st, const Lds& s, bool odd) {
     const uint32_t me = odd ? fbits(h.h0.y) : fbits(h.h0.x);
     const float alpha_tilde = h.v1.w;
     const float inv_mass = h.mi.x;
@@ -266,9 +277,8 @@ __device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const Lds& 
     const float sg = odd ? -1.0f : 1.0f;
     const f3 axis_local = xyz(h.v1);
     const float lower = h.v2.x, upper = h.v2.y;
-    const q4 Q = toq(s.quat[me]);
-    const q4 Qo = pair_swap(Q);
-    const q4 qa = sel(odd, Qo, Q), qb = sel(odd, Q, Qo);
+    const q4 Q = toq(st.Q);
+    const q4 qa = pair_a(Q), qb = pair_b(Q);
     const q4 q_rel = qmul(qconj(qa), qb);
     const float angle = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
     float violation = 0.0f;
@@ -281,7 +291,7 @@ __device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const Lds& 
         if (w > 1e-8f) {
             const float d_lambda = violation / (w + alpha_tilde);
             const f3 ang_impulse = sscale(d_lambda, aw);
-            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, signed4(sg, qdelta(mul(ang_impulse, iI), Q)))));
+            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, qdelta_signed(mul(ang_impulse, iI), Q, sg))));
         }
     }
 }
@@ -485,8 +495,7 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
     const f3 r = sub(cp, xyz(P0));
     const f3 vpt = add(xyz(V0), cross(xyz(W0), r));
     asm volatile("" : "+v"(jn_prev));
-    const f3 vpo = pair_swap(vpt);
-    const f3 rel_vel = sub(sel(odd, vpo, vpt), sel(odd, vpt, vpo));
+    const f3 rel_vel = sub(pair_a(vpt), pair_b(vpt));
     const float vel_normal = dot(rel_vel, normal);
     const f3 vel_tangent = sub(rel_vel, sscale(vel_normal, normal));
     const float tangent_speed = len(vel_tangent);
@@ -501,10 +510,11 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
     j_n = fmaxf(j_n, 0.0f);
     const f3 impulse_n = sscale(j_n, normal);
     f3 v = xyz(V0), w = xyz(W0);
+    const f3 siI = sscale(sg, iI);
     if (inv_mass > 1e-8f) {
-        v = add(v, signed3(sg, scale(impulse_n, inv_mass)));
-        w = add(w, signed3(sg, mul(cross(r, impulse_n), iI)));
-        set_xyz(&s.pos[me], add(xyz(P0), signed3(sg, sscale(odd ? aux.z : aux.y, normal))));
+        v = add(v, scale(impulse_n, sg * inv_mass));
+        w = add(w, mul(cross(r, impulse_n), siI));
+        set_xyz(&s.pos[me], add(xyz(P0), sscale(sg * (odd ? aux.z : aux.y), normal)));
     }
     const float j_n_acc = jn_prev + j_n;
     if (tangent_speed > 1e-6f && j_n_acc > 1e-6f) {
@@ -516,8 +526,8 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
             const float j_t = fminf(tangent_speed / w_tangent, friction * j_n_acc);
             const f3 impulse_t = sscale(j_t, tangent);
             if (inv_mass > 1e-8f) {
-                v = add(v, signed3(-sg, scale(impulse_t, inv_mass)));
-                w = add(w, signed3(-sg, mul(cross(r, impulse_t), iI)));
+                v = add(v, scale(impulse_t, -sg * inv_mass));
+                w = add(w, mul(cross(r, impulse_t), neg(siI)));
             }
         }
     }
@@ -525,7 +535,7 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
         set_xyz(&s.vel[me], v);
         set_xyz(&s.angvel[me], w);
     }
-    if (!odd) cr->impulses[0] = j_n;
+    cr->impulses[0] = j_n;  // both lanes store the same value
 }
 
 __device__ __forceinline__ void solve_contact2(const Mdl& md, const Lds& s, uint32_t phys, bool odd) {
@@ -617,13 +627,15 @@ __device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, Cont
     }
 }
 
-// One joint solve of the given type on the lane pair: h is the lane's half record (lane-pair
-// types), r the whole record in LDS (single-lane types, run by body a's lane).
-__device__ __forceinline__ void solve_joint(uint32_t type, const JHalf& h, const float4* r, const Lds& s, bool odd) {
+// One joint solve of the given type on the lane pair: h is the lane's half record and st its
+// body's state (lane-pair types), r the whole record in LDS (single-lane types, run by body
+// a's lane, which read the state themselves).
+__device__ __forceinline__ void solve_joint(uint32_t type, const JHalf& h, const JState& st, const float4* r, const Lds& s,
+                                            bool odd) {
     switch (type) {
-        case C_POSITIONAL: solve_positional2(h, s, odd); break;
-        case C_ANGULAR: solve_angular2(h, s, odd); break;
-        case C_ANGULAR_LIMIT: solve_angular_limit2(h, s, odd); break;
+        case C_POSITIONAL: solve_positional2(h, st, s, odd); break;
+        case C_ANGULAR: solve_angular2(h, st, s, odd); break;
+        case C_ANGULAR_LIMIT: solve_angular_limit2(h, st, s, odd); break;
         case C_WELD: if (!odd) solve_weld(r, s); break;
         case C_LINEAR_LIMIT: if (!odd) solve_linear_limit(r, s); break;
         case C_SLIDER: if (!odd) solve_slider(r, s); break;
@@ -1552,11 +1564,12 @@ void step_kernel(StepArgs a) {
                     const uint32_t st = __builtin_amdgcn_readfirstlane(ph1.start), cn = __builtin_amdgcn_readfirstlane(ph1.count);
                     nxt = load_half(md.jrec + (st + (kf < cn ? kf : 0u)) * kJRecQuads + half);
                 }
-                if (live && kf < cnt) solve_joint(type, cur, md.jrec + (start + kf) * kJRecQuads, s, odd);
+                if (live && kf < cnt) solve_joint(type, cur, load_jstate(cur, s, odd), md.jrec + (start + kf) * kJRecQuads, s, odd);
                 if (live) {
                     for (uint32_t k = kf + G / 2; k < cnt; k += G / 2) {
                         const float4* r = md.jrec + (start + k) * kJRecQuads;
-                        solve_joint(type, load_half(r + half), r, s, odd);
+                        const JHalf hk = load_half(r + half);
+                        solve_joint(type, hk, load_jstate(hk, s, odd), r, s, odd);
                     }
                 }
                 wave_sync<HBM>();
@@ -1861,7 +1874,7 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStrea
                               : launch_as<1, PL_MODEL_HBM, false, true>(a, blocks, env_lds, stream);
             case PL_LDS:
                 return a.hash ? launch_as<1, PL_LDS, true, true>(a, blocks, shmem, stream)
-                              : launch_as<1, PL_LDS, false, true>(a, blocks, shmem, stream);
+                              : launch_as<1, PL_LDS, false, true>(a, blocks, shmem, stream, waves);
             default: return hipErrorInvalidValue;
         }
     }
