@@ -90,9 +90,15 @@ int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, ui
  * per workgroup (with the working sets in HBM, the contact and hash arrays kept in LDS). */
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
 
-/* Waves per workgroup of the world's step launches (1..4; with the model records in LDS, the
- * waves of a workgroup share one copy of them). 0 for an invalid handle. */
+/* Environment groups per workgroup of the world's step launches (1..4; with the model records
+ * in LDS, the groups of a workgroup share one copy of them), one wave each, or two with split
+ * groups. 0 for an invalid handle. */
 uint32_t zeno_amd_world_waves_per_group(ZenoWorldHandle world);
+
+/* No counterpart in the reference (a launch-shape query). 1 when each environment group runs
+ * on two waves: one solving the joints and contacts, one running the contact pipeline (broad
+ * phase to contact levels) meanwhile; 0 when one wave does both; -1 for an invalid handle. */
+int zeno_amd_world_split_groups(ZenoWorldHandle world);
 
 /* *placement: where the step kernel keeps the scene's model records and each environment's
  * working set. 0 = both in LDS (several environments per workgroup); 1 = model records read

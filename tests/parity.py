@@ -78,14 +78,17 @@ def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, ato
 
 def make_pair(name: str, num_envs: int, steps: int, seed: int = 0, envs_per_wave: Optional[int] = None,
               substeps: int = 1, max_contacts: int = 64, contact_iterations: int = 4,
-              placement: Optional[int] = None, extended_contacts: bool = False, waves: Optional[int] = None):
-    """GPU world and oracle on the same seeded state. envs_per_wave / waves (per workgroup) /
-    placement (1: model records in HBM, 2: working sets in HBM too) override the launch shape
-    the world would choose; extended_contacts turns on the extended-contact mode on both."""
+              placement: Optional[int] = None, extended_contacts: bool = False, waves: Optional[int] = None,
+              split: Optional[bool] = None):
+    """GPU world and oracle on the same seeded state. envs_per_wave / waves (environment groups
+    per workgroup) / split (two waves per group) / placement (1: model records in HBM, 2:
+    working sets in HBM too) override the launch shape the world would choose;
+    extended_contacts turns on the extended-contact mode on both."""
     path, xml, model, state, acts = workload_inputs(name, num_envs, steps, seed)
     overrides = {"ZENO_AMD_ENVS_PER_WAVE": None if envs_per_wave is None else str(envs_per_wave),
                  "ZENO_AMD_PLACEMENT": None if placement is None else str(placement),
-                 "ZENO_AMD_WAVES": None if waves is None else str(waves)}
+                 "ZENO_AMD_WAVES": None if waves is None else str(waves),
+                 "ZENO_AMD_SPLIT": None if split is None else ("1" if split else "0")}
     saved = {k: os.environ.get(k) for k in overrides}
     try:
         for k, v in overrides.items():

@@ -74,6 +74,34 @@ def test_multi_wave_workgroups_agree(name, envs, epw, waves):
         compare(gpu_arrays(g), oracle_arrays(o), **ONE_STEP)
 
 
+@pytest.mark.parametrize("name,envs,epw,waves,substeps", [("ant", 37, 4, 4, 1), ("ant", 20, 2, 2, 1),
+                                                          ("humanoid", 21, 4, 4, 1), ("pendulum", 9, 1, 4, 1),
+                                                          ("cartpole", 13, 2, 4, 3), ("pile", 5, 1, 2, 2)])
+def test_split_groups_agree(name, envs, epw, waves, substeps):
+    """Two waves per environment group: the helper runs the snapshot, broad phase, sort,
+    narrow phase, matching and levels on the poses after integration while the solver runs the
+    joints, and writes the contact list back; several substeps (three barriers each) and env
+    counts that leave the last workgroup partly empty included."""
+    g, o, acts = make_pair(name, envs, 6, seed=23, envs_per_wave=epw, waves=waves, split=True, substeps=substeps)
+    assert g.launch_config()[0] == epw and g.waves_per_group() == waves and g.split_groups()
+    for k in range(6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), **ONE_STEP)
+
+
+def test_split_groups_subset_and_extended_contacts():
+    """Split groups with a step subset (the helper records the advanced contact list of the
+    environments not stepped) and with the extended-contact narrow phase."""
+    g, o, acts = make_pair("ant", 12, 4, seed=29, envs_per_wave=4, waves=2, split=True, extended_contacts=True)
+    assert g.split_groups()
+    mask = (np.arange(12) % 3 != 0).astype(np.uint8)
+    for k in range(4):
+        g.step_subset(acts[k], mask) if k % 2 else g.step(acts[k])
+        o.step_subset(acts[k], mask) if k % 2 else o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("waves", [2, 4])
 def test_grouped_narrow_phase_multi_wave(waves):
     """Extended-contact mode at one environment per wave launches the narrow-phase instance

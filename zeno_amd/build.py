@@ -56,14 +56,16 @@ RESOURCES = BUILD / "step_resources.txt"
 def step_occupancy(remarks: str) -> dict[str, int]:
     """Waves per SIMD of each step-kernel variant, from the compiler's kernel-resource-usage
     remarks, keyed "EPW,PL,HASH" (and "EPW,PL,HASH,grouped" for the instances whose narrow
-    phase visits the slots grouped by geom-type pair). The one-environment-per-wave shapes (EPW 1) rely on two
-    resident waves per SIMD to hide memory latency; a change that pushes one of them past
-    256 registers can halve its throughput (the rigid pile's placement-1 kernel: 2.7x)."""
+    phase visits the slots grouped by geom-type pair, "EPW,PL,HASH,split" for the instances
+    with two waves per environment group). The one-environment-per-wave shapes (EPW 1) rely on
+    two resident waves per SIMD to hide memory latency; a change that pushes one of them past
+    256 registers can halve its throughput (the rigid pile's placement-1 kernel: 2.7x). The
+    split instances need two per SIMD to hold a group's two waves on one SIMD."""
     occ, name = {}, None
     for line in remarks.splitlines():
-        m = re.search(r"Function Name: \S*step_kernelILi(\d+)ELi(\d+)ELb(\d)E(?:Lb(\d)E)?", line)
+        m = re.search(r"Function Name: \S*step_kernelILi(\d+)ELi(\d+)ELb(\d)E(?:Lb(\d)E)?(?:Lb(\d)E)?", line)
         if m:
-            name = ",".join(m.groups()[:3]) + (",grouped" if m.group(4) == "1" else "")
+            name = ",".join(m.groups()[:3]) + (",grouped" if m.group(4) == "1" else "") + (",split" if m.group(5) == "1" else "")
             continue
         m = re.search(r"Occupancy \[waves/SIMD\]: (\d+)", line)
         if m and name:

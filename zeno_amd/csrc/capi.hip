@@ -426,6 +426,7 @@ int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave,
 }
 
 uint32_t zeno_amd_world_waves_per_group(ZenoWorldHandle world) { return world ? (uint32_t)W(world)->waves : 0u; }
+int zeno_amd_world_split_groups(ZenoWorldHandle world) { return world ? (W(world)->split ? 1 : 0) : -1; }
 
 int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash) {
     if (!world) return ZENO_INVALID_HANDLE;

@@ -353,11 +353,14 @@ size_t max_lds_per_workgroup(int device);
 
 // Step-kernel workgroups one CU holds at once for a launch shape (LDS and register
 // limits, from the HIP occupancy query); 0 when the shape cannot launch.
-int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem, int waves = 1);
+// split: two waves per environment group (step_kernel's SPLIT instances); waves counts the
+// groups of a workgroup either way.
+int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem, int waves = 1, bool split = false);
 
-// Launches ceil(E / (envs_per_wave * waves)) workgroups of `waves` waves. envs_per_wave in
-// {1,2,4,8} and waves in 1..4; both 1 unless a.placement is PL_LDS and the hash is off.
-hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStream_t stream);
+// Launches ceil(E / (envs_per_wave * waves)) workgroups of `waves` environment groups, one
+// wave per group (two with split). envs_per_wave in {1,2,4,8} and waves in 1..4; both 1 and
+// split off unless a.placement is PL_LDS and the hash is off.
+hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStream_t stream, bool split = false);
 
 
 }  // namespace za

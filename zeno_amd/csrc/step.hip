@@ -742,28 +742,43 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
 // other shapes' register allocation is not touched by it.
 // The waves of a workgroup meet at one barrier, after the model records are in LDS; from
 // there each wave steps its own environments and synchronises with itself only.
+// SPLIT: two waves per group of EPW environments, on the same SIMD (wave w and wave w + NG of
+// a workgroup of 2 NG waves). The solver wave runs stages A-D, the joint and contact solves
+// and the post-solve stages; the helper wave runs the snapshot, the broad phase, the sort, the
+// narrow phase, the cache matching and the contact levels while the solver runs the joints
+// (these read the poses after integration and write nothing the joint solve reads), and
+// writes the contact list back while the solver finishes. The solver leaves the poses after
+// integration in the force and torque arrays (dead until the next substep) for the helper, as
+// the joint solve moves the bodies meanwhile. Three workgroup barriers per substep order the
+// two: after integration, before the contact solve and after it.
 // Two waves per SIMD at most 256 registers: the one-environment shapes hide their memory
 // latency with a second resident wave, and more than 256 registers would leave one.
-template <int EPW, int PL, bool HASH, bool GROUP>
-__global__ __launch_bounds__(PL == PL_LDS && !HASH ? kMaxWaves * kWave : kWave) __attribute__((amdgpu_waves_per_eu(2)))
+template <int EPW, int PL, bool HASH, bool GROUP, bool SPLIT = false>
+__global__ __launch_bounds__(SPLIT ? 2 * kMaxWaves * kWave : (PL == PL_LDS && !HASH ? kMaxWaves * kWave : kWave))
+__attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
     constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     static_assert(!GROUP || EPW == 1, "type-grouped narrow phase: one environment per workgroup");
+    static_assert(!SPLIT || (PL == PL_LDS && !HASH && !GROUP), "split groups: working sets and model in LDS");
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = (int)(threadIdx.x & (kWave - 1));    // lane
     constexpr bool MULTI = PL == PL_LDS && !HASH;          // several waves per workgroup possible
     const uint32_t wv = MULTI ? threadIdx.x / kWave : 0u;  // wave in this workgroup
     const uint32_t W = MULTI ? blockDim.x / kWave : 1u;    // waves in this workgroup
-    const uint32_t wave_id = blockIdx.x * W + wv;
+    const uint32_t NG = SPLIT ? W / 2u : W;                 // environment groups in this workgroup
+    const bool helper = SPLIT && wv >= NG;                  // split: the group's second wave
+    const bool do_solve = !helper, do_prep = !SPLIT || helper;
+    const uint32_t grp = SPLIT ? wv % NG : wv;              // this wave's group in the workgroup
+    const uint32_t wave_id = blockIdx.x * NG + grp;         // environment group
     const int le = tid / G;
     const int sl = tid % G;
     const uint32_t env = wave_id * EPW + le;
     const bool live = env < a.E;
     unsigned char* const env_base = HBM ? a.work + (size_t)wave_id * a.lds.bytes
-                                        : smem + (PL == PL_LDS ? a.ml.bytes : 0u) + wv * EPW * a.lds.bytes;
+                                        : smem + (PL == PL_LDS ? a.ml.bytes : 0u) + grp * EPW * a.lds.bytes;
     Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
     if (HBM) bind_small(s, smem, a.lds_small);
     bind_levels(s, a.M);
@@ -805,14 +820,14 @@ void step_kernel(StepArgs a) {
     uint32_t count = 0, pcount = 0;
     bool detached = false;
     // The lane's first action (read by stage A of every substep) is loaded with the state.
-    const float act0 = (live && (uint32_t)sl < a.A) ? a.actions[(size_t)env * a.A + sl] : 0.0f;
+    const float act0 = (live && do_solve && (uint32_t)sl < a.A) ? a.actions[(size_t)env * a.A + sl] : 0.0f;
     const size_t eb = (size_t)env * B;
     const ContactRec* gc = a.contacts + (size_t)env * M;
     const uint32_t b0 = sl, j0 = sl;
     float4 p_pos = make_float4(0, 0, 0, 0), p_quat = p_pos, p_vel = p_pos, p_ang = p_pos;
     float p_jt = 0.0f, p_lam = 0.0f;
     Slot4 c0{}, c1{}, c2{}, c3{};
-    if (live) {
+    if (live && do_solve) {
         if (b0 < B) {
             p_pos = a.pos[eb + b0];
             p_quat = a.quat[eb + b0];
@@ -821,6 +836,8 @@ void step_kernel(StepArgs a) {
         }
         if (j0 < Jp) p_jt = a.jtrq[(size_t)env * Jp + j0];
         if (j0 < N) p_lam = a.lam[(size_t)env * N + j0];
+    }
+    if (live && do_prep) {
         if (sl < M) c0 = read_slot(&gc[sl]);
         if (sl + G < M) c1 = read_slot(&gc[sl + G]);
         if (sl + 2 * G < M) c2 = read_slot(&gc[sl + 2 * G]);
@@ -877,7 +894,7 @@ void step_kernel(StepArgs a) {
         fill_alpha(threadIdx.x, blockDim.x);  // the workgroup's one copy of the records
     }
 
-    if (live) {
+    if (live && do_solve) {
         if (b0 < B) {
             s.pos[b0] = p_pos;
             s.quat[b0] = p_quat;
@@ -897,6 +914,8 @@ void step_kernel(StepArgs a) {
         if (j0 < N) s.lam[j0] = p_lam;
         for (uint32_t j = sl + G; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
         for (uint32_t i = sl + G; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
+    }
+    if (live && do_prep) {
         if (sl < M) { write_slot(&s.con[sl], c0); s.perm[sl] = (uint16_t)sl; }
         if (sl + G < M) { write_slot(&s.con[sl + G], c1); s.perm[sl + G] = (uint16_t)(sl + G); }
         if (sl + 2 * G < M) { write_slot(&s.con[sl + 2 * G], c2); s.perm[sl + 2 * G] = (uint16_t)(sl + 2 * G); }
@@ -907,13 +926,13 @@ void step_kernel(StepArgs a) {
             s.perm[k] = (uint16_t)k;
         }
     }
-    __syncthreads();  // the last barrier of the workgroup: below, each wave syncs with itself
+    __syncthreads();  // below, each wave syncs with itself (split groups: three barriers per substep)
     if (PL != PL_LDS) fill_alpha(tid, kWave);
     tick(PH_LOAD);
 
     for (uint32_t step = 0; step < a.substeps; ++step) {
         // ---- Previous-contact snapshot (cache_contacts of the last substep) -----------
-        if (live) {
+        if (live && do_prep) {
             const uint32_t pn = pcount < M ? pcount : M;
             const bool from_det = step == 0 && detached;
             for (uint32_t k = sl; k < pn; k += G) {
@@ -927,7 +946,7 @@ void step_kernel(StepArgs a) {
         // body compute_forces and update_kinematic in dispatch order (:345-388, :304-339,
         // world.zig:962-990: the torque reads the quaternion before a kinematic body's
         // update) and save_prev_state (:1900-1913). Each lane touches only its own entries.
-        if (live) {
+        if (live && do_solve) {
             for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
             for (uint32_t k = sl; k < a.A; k += G) {
                 const ActuatorRec& act = md.acts[k];
@@ -966,7 +985,7 @@ void step_kernel(StepArgs a) {
         // Each joint's world-frame contribution axis_world * tau is formed by one lane into
         // jw (skipped when |tau| < 1e-6, flag w = 0); then each body sums the contributions
         // of its joints in ascending joint order (build_body_joint_lists), and integrates.
-        if (live) {
+        if (live && do_solve) {
             for (uint32_t j = sl; j < a.J; j += G) {
                 const JointRec& jr = md.joints[j];
                 const float tau = s.jt[j];
@@ -980,10 +999,13 @@ void step_kernel(StepArgs a) {
         }
         wave_sync<HBM>();
         // ---- D: integrate (:394-462), on the lane that formed the body's forces -----------
-        if (live) {
+        if (live && do_solve) {
             for (uint32_t b = sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
-                if (imi.x < 1e-8f) continue;
+                if (imi.x < 1e-8f) {
+                    if (SPLIT) { s.frc[b] = s.pos[b]; s.trq[b] = s.quat[b]; }  // the helper's pose copy
+                    continue;
+                }
                 float4 f = s.frc[b], t = s.trq[b];
                 const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
                 for (uint32_t e = e0; e < e1; ++e) {
@@ -1007,11 +1029,20 @@ void step_kernel(StepArgs a) {
                 q = qnormalize(q);
                 s.angvel[b] = tof4(om, 0.0f);
                 s.quat[b] = tof4(q);
+                if (SPLIT) { s.frc[b] = tof4(pos, 0.0f); s.trq[b] = tof4(q); }  // the helper's pose copy
             }
         }
         wave_sync<HBM>();
         tick(PH_FORCES);
+        if (SPLIT) __syncthreads();  // split barrier 1: poses after integration are in place
         // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
+        // Broad phase to contact levels: the helper's part of a split group, on the poses
+        // after integration (the force and torque arrays hold them; the level masks overwrite
+        // them after the narrow phase).
+        if (do_prep) {
+        Lds sp = s;
+        if (SPLIT) { sp.pos = s.frc; sp.quat = s.trq; }
+        Lds& s = sp;
         const uint32_t count_before = count;
         if (HASH) {
             uint4* const hmeta = (uint4*)(s.hpos + a.G);
@@ -1526,12 +1557,7 @@ void step_kernel(StepArgs a) {
             }
         }
         wave_sync<HBM>();
-        uint32_t max_lev = 0;
-        for (int e2 = 0; e2 < EPW; ++e2) {
-            const uint32_t* m2 = HBM ? s.misc : (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
-            if (wave_id * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
-        }
-        const uint32_t my_nlev = live ? s.misc[2] : 0u;
+        }  // do_prep
         tick(PH_NARROW);
         // ---- H: solve_joints, iterations x colours (world.zig:1163-1195, S3) ----------
         // Phases are same-type runs inside a colour (build_joint_program); the type is
@@ -1540,7 +1566,7 @@ void step_kernel(StepArgs a) {
         // solve records are read-only, so while phase t runs, the descriptor of phase t + 2
         // and the lane's first solve record of phase t + 1 are loaded; a phase then starts
         // with only its bodies' state to read.
-        {
+        if (do_solve) {
             const uint32_t nph = a.iters * a.njph;
             const uint32_t kf = (uint32_t)sl >> 1;
             const bool odd = (sl & 1) != 0;
@@ -1586,13 +1612,20 @@ void step_kernel(StepArgs a) {
             if (t < nph) phase(rec, rec2);
         }
         tick(PH_JOINTS);
+        if (SPLIT) __syncthreads();  // split barrier 2: the contact levels are in place
+        uint32_t max_lev = 0;
+        for (int e2 = 0; e2 < EPW; ++e2) {
+            const uint32_t* m2 = HBM ? s.misc : (const uint32_t*)(env_base + e2 * a.lds.bytes + a.lds.misc);
+            if (wave_id * EPW + e2 < a.E && m2[2] > max_lev) max_lev = m2[2];
+        }
+        const uint32_t my_nlev = live ? s.misc[2] : 0u;
         // ---- I: solve_contacts, iterations x levels (world.zig:1199-1213, S4) --------
         // Lane pair (2k, 2k+1) takes the k-th slot of each level (and k + G/2, ... when a
         // level holds more). The level lists and the slots' static parts are read ahead over
         // the sequence of (iteration, level) steps: at step f the lane's slot record of step
         // f + 1, its slot index of step f + 2 and the level bounds of step f + 3 are loaded,
         // so a step starts with its record in registers and reads only the bodies' state.
-        if (max_lev > 0) {
+        if (do_solve && max_lev > 0) {
             const bool odd = (sl & 1) != 0;
             const uint32_t kf = (uint32_t)sl >> 1;
             const uint32_t nsteps = a.iters * max_lev;
@@ -1646,8 +1679,9 @@ void step_kernel(StepArgs a) {
             if (f < nsteps) cstep(f, cA, cB);
         }
         tick(PH_CONTACTS);
+        if (SPLIT) __syncthreads();  // split barrier 3: the contact list is final for this substep
         // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
-        if (live) {
+        if (live && do_solve) {
             const float inv_dt = 1.0f / a.dt;
             for (uint32_t b = sl; b < B; b += G) {
                 if (md.invmi[b].x < 1e-8f) continue;
@@ -1659,7 +1693,7 @@ void step_kernel(StepArgs a) {
         }
         wave_sync<HBM>();
         // ---- K: update_joint_states (:1550-1638) ------------------------------------
-        if (live) {
+        if (live && do_solve) {
             for (uint32_t j = sl; j < a.J; j += G) {
                 const JointRec& jr = md.joints[j];
                 const uint32_t type = (uint32_t)jr.params[0];
@@ -1689,7 +1723,7 @@ void step_kernel(StepArgs a) {
         // ---- L: read_sensors (:1799-1893); cache_contacts is the next snapshot --------
         // The row is assembled in the working set and written back with the state. Entries
         // that no sensor writes are 0 (nothing else ever writes the observation buffer).
-        if (stepped && step + 1 == a.substeps) {
+        if (stepped && do_solve && step + 1 == a.substeps) {
             float* obs = s.obs;
             for (uint32_t k = sl; k < a.obsp; k += G) obs[k] = 0.0f;
             wave_sync<HBM>();
@@ -1724,6 +1758,7 @@ void step_kernel(StepArgs a) {
     if (stepped) {
         const size_t eb = (size_t)env * B;
         const StepArgs::HostViews& hv = a.hv;
+        if (do_solve) {
         for (uint32_t b = sl; b < B; b += G) {
             const float4 p = s.pos[b], q = s.quat[b], v = s.vel[b], v0 = s.vb[b], w = s.angvel[b];
             const float4 acc = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
@@ -1752,6 +1787,8 @@ void step_kernel(StepArgs a) {
             a.obs[o] = s.obs[k];
             if (hv.obs) hv.obs[o] = s.obs[k];
         }
+        }  // do_solve
+        if (do_prep) {
         ContactRec* gc = a.contacts + (size_t)env * M;
         for (uint32_t k = sl; k < n_out; k += G) {
             const float4* src = (const float4*)&s.con[s.perm[k]];
@@ -1767,7 +1804,8 @@ void step_kernel(StepArgs a) {
             a.counts[env] = count;
             if (hv.counts) hv.counts[env] = count;
         }
-    } else {
+        }  // do_prep
+    } else if (do_prep) {
         // Not advanced: keep visible state, record the advanced contact list as the
         // previous-contact snapshot (world.zig:880-928 restores everything else).
         ContactRec* pc = a.prev_out + (size_t)env * M;
@@ -1777,8 +1815,10 @@ void step_kernel(StepArgs a) {
             d[0] = src[0]; d[1] = src[1]; d[2] = src[2]; d[3] = src[3];
         }
     }
-    for (uint32_t i = sl; i < N; i += G) a.lam[(size_t)env * N + i] = s.lam[i];
-    if (sl == 0) {
+    if (do_solve) {
+        for (uint32_t i = sl; i < N; i += G) a.lam[(size_t)env * N + i] = s.lam[i];
+    }
+    if (do_prep && sl == 0) {
         a.pcounts[env] = count;
         if (a.prev_detached_out) a.prev_detached_out[env] = stepped ? 0 : 1;
     }
@@ -1794,34 +1834,36 @@ void step_kernel(StepArgs a) {
         if (_e != hipSuccess) return _e; \
     } while (0)
 
-template <int EPW, int PL, bool HASH, bool GROUP = false>
+template <int EPW, int PL, bool HASH, bool GROUP = false, bool SPLIT = false>
 hipError_t allow_lds(size_t shmem) {
     // Workgroups above 64 KB of dynamic LDS must opt in per kernel (gfx950 has 160 KB / CU).
     static size_t granted = 64 * 1024;
     if (shmem <= granted) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, PL, HASH, GROUP>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+    hipError_t e = hipFuncSetAttribute((const void*)step_kernel<EPW, PL, HASH, GROUP, SPLIT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
     if (e == hipSuccess) granted = shmem;
     return e;
 }
 
-template <int EPW, int PL, bool HASH, bool GROUP = false>
+template <int EPW, int PL, bool HASH, bool GROUP = false, bool SPLIT = false>
 int resident_as(size_t shmem, int waves = 1) {
     // A shape that does not fit is an answer here, not an error: the failed query's error
     // is taken off HIP's last-error slot so that later hipGetLastError checks (of this or
     // another world) do not report it.
     int n = 0;
-    if (allow_lds<EPW, PL, HASH, GROUP>(shmem) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH, GROUP>, kWave * waves, shmem) != hipSuccess) {
+    if (allow_lds<EPW, PL, HASH, GROUP, SPLIT>(shmem) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, step_kernel<EPW, PL, HASH, GROUP, SPLIT>, kWave * waves, shmem) !=
+            hipSuccess) {
         (void)hipGetLastError();
         return 0;
     }
     return n;
 }
 
-template <int EPW, int PL, bool HASH, bool GROUP = false>
+template <int EPW, int PL, bool HASH, bool GROUP = false, bool SPLIT = false>
 hipError_t launch_as(const StepArgs& a, uint32_t blocks, size_t shmem, hipStream_t stream, int waves = 1) {
-    ZA_CHECK((allow_lds<EPW, PL, HASH, GROUP>(shmem)));
-    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH, GROUP>), dim3(blocks), dim3(kWave * waves), shmem, stream, a);
+    ZA_CHECK((allow_lds<EPW, PL, HASH, GROUP, SPLIT>(shmem)));
+    hipLaunchKernelGGL((step_kernel<EPW, PL, HASH, GROUP, SPLIT>), dim3(blocks), dim3(kWave * waves), shmem, stream, a);
     return hipGetLastError();
 }
 
@@ -1833,14 +1875,23 @@ size_t max_lds_per_workgroup(int device) {
     return (size_t)v;
 }
 
-int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem, int waves) {
+int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t shmem, int waves, bool split) {
     if (waves < 1 || waves > kMaxWaves) return 0;
     if (hash || placement != PL_LDS) {
-        if (envs_per_wave != 1 || waves != 1) return 0;
+        if (envs_per_wave != 1 || waves != 1 || split) return 0;
         switch (placement) {
             case PL_LDS: return resident_as<1, PL_LDS, true>(shmem);
             case PL_MODEL_HBM: return hash ? resident_as<1, PL_MODEL_HBM, true>(shmem) : resident_as<1, PL_MODEL_HBM, false>(shmem);
             case PL_ALL_HBM: return hash ? resident_as<1, PL_ALL_HBM, true>(shmem) : resident_as<1, PL_ALL_HBM, false>(shmem);
+            default: return 0;
+        }
+    }
+    if (split) {
+        switch (envs_per_wave) {
+            case 1: return resident_as<1, PL_LDS, false, false, true>(shmem, 2 * waves);
+            case 2: return resident_as<2, PL_LDS, false, false, true>(shmem, 2 * waves);
+            case 4: return resident_as<4, PL_LDS, false, false, true>(shmem, 2 * waves);
+            case 8: return resident_as<8, PL_LDS, false, false, true>(shmem, 2 * waves);
             default: return 0;
         }
     }
@@ -1853,9 +1904,10 @@ int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t
     }
 }
 
-hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStream_t stream) {
+hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStream_t stream, bool split) {
     if (a.E == 0) return hipSuccess;
     if (waves < 1 || waves > kMaxWaves) return hipErrorInvalidValue;
+    if (split && (a.placement != PL_LDS || a.hash)) return hipErrorInvalidValue;
     const uint32_t per_group = (uint32_t)envs_per_wave * (uint32_t)waves;
     const uint32_t blocks = (a.E + per_group - 1) / per_group;
     if ((a.placement != PL_LDS || a.hash) && (envs_per_wave != 1 || waves != 1)) return hipErrorInvalidValue;
@@ -1864,7 +1916,7 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStrea
     const size_t shmem = (size_t)a.ml.bytes + env_lds * (size_t)waves;
     // Extended-contact mode with one environment per workgroup: the instance whose narrow
     // phase visits the slots grouped by geom-type pair (same results, less divergence).
-    if (a.ext_contacts && a.M >= 64 && envs_per_wave == 1) {
+    if (a.ext_contacts && a.M >= 64 && envs_per_wave == 1 && !split) {
         switch (a.placement) {
             case PL_ALL_HBM:
                 return a.hash ? launch_as<1, PL_ALL_HBM, true, true>(a, blocks, a.lds_small.bytes, stream)
@@ -1889,6 +1941,15 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStrea
         default: return hipErrorInvalidValue;
     }
     if (a.hash) return launch_as<1, PL_LDS, true>(a, blocks, shmem, stream);
+    if (split) {
+        switch (envs_per_wave) {
+            case 1: return launch_as<1, PL_LDS, false, false, true>(a, blocks, shmem, stream, 2 * waves);
+            case 2: return launch_as<2, PL_LDS, false, false, true>(a, blocks, shmem, stream, 2 * waves);
+            case 4: return launch_as<4, PL_LDS, false, false, true>(a, blocks, shmem, stream, 2 * waves);
+            case 8: return launch_as<8, PL_LDS, false, false, true>(a, blocks, shmem, stream, 2 * waves);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (envs_per_wave) {
         case 1: return launch_as<1, PL_LDS, false>(a, blocks, shmem, stream, waves);
         case 2: return launch_as<2, PL_LDS, false>(a, blocks, shmem, stream, waves);

@@ -32,7 +32,8 @@ struct World {
     float gravity[3] = {0, 0, -9.81f};
     int device = 0;
     int epw = 1;
-    int waves = 1;  // waves per workgroup (model records in LDS: one copy per workgroup)
+    int waves = 1;  // environment groups (waves) per workgroup (model records in LDS: one copy per workgroup)
+    bool split = false;  // two waves per group: the solver and the helper (step_kernel SPLIT)
     EnvLds lds{};
     EnvLds lds_small{};  // placement 2: the arrays kept in LDS
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)

@@ -179,8 +179,12 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     // Ant 4096 79.6 against 80.0 us per step), and among the LDS shapes first the largest
     // environments-per-wave with at least 1024 workgroups and 64 KB of LDS, then the others
     // from 1 up.
-    // ZENO_AMD_PLACEMENT=0/1/2, ZENO_AMD_ENVS_PER_WAVE and ZENO_AMD_WAVES force a placement
-    // or a shape (tests of each path; a forced shape implies placement 0).
+    // Each LDS shape also comes split, and ties prefer it: two waves per environment group,
+    // the second running the contact pipeline (broad phase to contact levels) while the first
+    // solves the joints; same LDS, twice the waves (Ant 4096 74.4 -> 66.2 us per step,
+    // Humanoid 16384 266 -> 232 us).
+    // ZENO_AMD_PLACEMENT=0/1/2, ZENO_AMD_ENVS_PER_WAVE, ZENO_AMD_WAVES and ZENO_AMD_SPLIT=0/1
+    // force a placement or a shape (tests of each path; a forced shape implies placement 0).
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
@@ -190,13 +194,14 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash, false);
     const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec,
                                       !w->hash, w->obsp);
-    struct Cand { uint32_t pl; int epw; int waves; size_t shmem; };
+    struct Cand { uint32_t pl; int epw; int waves; size_t shmem; bool split; };
     std::vector<Cand> cands;
-    int force_pl = -1, force_epw = 0, force_waves = 0;
+    int force_pl = -1, force_epw = 0, force_waves = 0, force_split = -1;
     if (const char* env = std::getenv("ZENO_AMD_PLACEMENT")) force_pl = std::min(std::max(std::atoi(env), 0), 2);
     if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) force_epw = std::atoi(env);
     if (const char* env = std::getenv("ZENO_AMD_WAVES")) force_waves = std::atoi(env);
-    if ((force_epw > 0 || force_waves > 1) && force_pl < 0) force_pl = PL_LDS;
+    if (const char* env = std::getenv("ZENO_AMD_SPLIT")) force_split = std::atoi(env) != 0 ? 1 : 0;
+    if ((force_epw > 0 || force_waves > 1 || force_split == 1) && force_pl < 0) force_pl = PL_LDS;
     {
         std::vector<int> order;
         for (int cand : {8, 4, 2}) {
@@ -210,15 +215,18 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
             if (cand > 1 && w->hash) continue;
             if (std::find(order.begin(), order.end(), cand) == order.end()) order.push_back(cand);
         }
-        for (int waves : {4, 1, 2}) {
-            if (waves > 1 && w->hash) continue;
-            for (int cand : order) {
-                const size_t shmem = (size_t)ML.bytes + (size_t)L.bytes * cand * waves;
-                if (shmem <= lds_max) cands.push_back({PL_LDS, cand, waves, shmem});
+        for (bool split : {true, false}) {
+            if (split && w->hash) continue;
+            for (int waves : {4, 1, 2}) {
+                if (waves > 1 && w->hash) continue;
+                for (int cand : order) {
+                    const size_t shmem = (size_t)ML.bytes + (size_t)L.bytes * cand * waves;
+                    if (shmem <= lds_max) cands.push_back({PL_LDS, cand, waves, shmem, split});
+                }
             }
         }
-        if ((size_t)L_own.bytes <= lds_max) cands.push_back({PL_MODEL_HBM, 1, 1, (size_t)L_own.bytes});
-        cands.push_back({PL_ALL_HBM, 1, 1, (size_t)L_small.bytes});
+        if ((size_t)L_own.bytes <= lds_max) cands.push_back({PL_MODEL_HBM, 1, 1, (size_t)L_own.bytes, false});
+        cands.push_back({PL_ALL_HBM, 1, 1, (size_t)L_small.bytes, false});
     }
     const Cand* best = nullptr;
     uint64_t best_score = 0;
@@ -226,7 +234,8 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         if (force_pl >= 0 && (int)c.pl != force_pl) continue;
         if (force_epw > 0 && c.epw != force_epw) continue;
         if (force_waves > 0 && c.waves != force_waves) continue;
-        const int n = resident_workgroups(c.epw, c.pl, w->hash, c.shmem, c.waves);
+        if (force_split >= 0 && c.split != (force_split == 1)) continue;
+        const int n = resident_workgroups(c.epw, c.pl, w->hash, c.shmem, c.waves, c.split);
         if (n <= 0) continue;
         const uint64_t score = std::min<uint64_t>(w->E, (uint64_t)n * (uint64_t)c.epw * (uint64_t)c.waves * (uint64_t)cus);
         if (!best || score > best_score) { best = &c; best_score = score; }
@@ -235,7 +244,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         err = "no launch shape fits this scene: the smallest per-environment LDS working set is " +
               std::to_string(L_small.bytes) + " bytes (contacts, sort keys, level masks for max_contacts_per_env=" +
               std::to_string(w->M) + "), a workgroup may use " + std::to_string(lds_max) +
-              " (or ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE / ZENO_AMD_WAVES force a shape that cannot launch)";
+              " (or ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE / ZENO_AMD_WAVES / ZENO_AMD_SPLIT force a shape that cannot launch)";
         delete w;
         return nullptr;
     }
@@ -246,6 +255,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->lds_small = L_small;
     w->epw = epw;
     w->waves = best->waves;
+    w->split = best->split;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
     if ((e = hipStreamCreateWithFlags(&w->view_stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
@@ -422,7 +432,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
         if (!prof_start) { ZA_TRY(hipEventCreate(&prof_start)); ZA_TRY(hipEventCreate(&prof_stop)); }
         ZA_TRY(hipEventRecord(prof_start, stream));
     }
-    ZA_TRY(launch_step(a, epw, waves, stream));
+    ZA_TRY(launch_step(a, epw, waves, stream, split));
     if (prof_events) { ZA_TRY(hipEventRecord(prof_stop, stream)); prof_pending = true; }
     if (timed) ZA_TRY(hipEventRecord(t1, stream));
     mark_all_dirty();

@@ -402,9 +402,14 @@ class ZenoWorld:
         return epw.value, lds.value
 
     def waves_per_group(self) -> int:
-        """Waves per workgroup of the step launches (the waves of a workgroup share one copy
-        of the model records in LDS)."""
+        """Environment groups per workgroup of the step launches (the groups of a workgroup
+        share one copy of the model records in LDS); one wave each, two when split."""
         return int(self._lib.zeno_amd_world_waves_per_group(self._handle))
+
+    def split_groups(self) -> bool:
+        """True when each environment group runs on two waves: one solving the joints and
+        contacts, one running the contact pipeline (broad phase to levels) meanwhile."""
+        return self._lib.zeno_amd_world_split_groups(self._handle) == 1
 
     def modes(self) -> Dict[str, Any]:
         """{"placement": 0 model + working sets in LDS, 1 model in HBM and working set in LDS,
