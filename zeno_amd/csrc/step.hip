@@ -849,10 +849,13 @@ void step_kernel(StepArgs a) {
     // With the model records in HBM, the working-set reads follow the copy of the solve
     // records and the geom staging without a barrier in between, so their HBM latencies
     // overlap.
-    if (PL == PL_LDS) {
+    // A split workgroup's solver waves copy the model records alone: a wave's loads return in
+    // order, so a helper's share of the copy would land only after its contact records.
+    const uint32_t copy_threads = SPLIT ? NG * kWave : blockDim.x;
+    if (PL == PL_LDS && threadIdx.x < copy_threads) {
         const uint32_t nq = a.ml.bytes / 16u;
         uint4* const dst = (uint4*)smem;
-        const uint32_t nt = blockDim.x;
+        const uint32_t nt = copy_threads;
         for (uint32_t i0 = threadIdx.x; i0 < nq; i0 += 4u * nt) {
             const uint32_t i1 = i0 + nt, i2 = i0 + 2u * nt, i3 = i0 + 3u * nt;
             const uint4 q0 = a.model[i0];
@@ -864,7 +867,7 @@ void step_kernel(StepArgs a) {
             if (i2 < nq) dst[i2] = q2;
             if (i3 < nq) dst[i3] = q3;
         }
-    } else {
+    } else if (PL != PL_LDS) {
         const uint4* src = a.model + a.ml.jrec / 16u;
         for (uint32_t i = tid; i < a.nrec * kJRecQuads; i += kWave) ((uint4*)s.jrec)[i] = src[i];
         if (!HASH) {
@@ -891,7 +894,7 @@ void step_kernel(StepArgs a) {
     };
     if (PL == PL_LDS) {
         __syncthreads();
-        fill_alpha(threadIdx.x, blockDim.x);  // the workgroup's one copy of the records
+        if (threadIdx.x < copy_threads) fill_alpha(threadIdx.x, copy_threads);  // the workgroup's one copy of the records
     }
 
     if (live && do_solve) {
@@ -915,7 +918,10 @@ void step_kernel(StepArgs a) {
         for (uint32_t j = sl + G; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
         for (uint32_t i = sl + G; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
     }
-    if (live && do_prep) {
+    // The contact list -> LDS. A split group's helper does this after the barrier: the solver
+    // does not read the list before the first barrier of the substep, so it starts on the
+    // bodies while the contact records (most of the bytes) are still arriving.
+    auto write_contacts = [&]() {
         if (sl < M) { write_slot(&s.con[sl], c0); s.perm[sl] = (uint16_t)sl; }
         if (sl + G < M) { write_slot(&s.con[sl + G], c1); s.perm[sl + G] = (uint16_t)(sl + G); }
         if (sl + 2 * G < M) { write_slot(&s.con[sl + 2 * G], c2); s.perm[sl + 2 * G] = (uint16_t)(sl + 2 * G); }
@@ -925,8 +931,10 @@ void step_kernel(StepArgs a) {
             write_slot(&s.con[k], read_slot(&gc[k]));
             s.perm[k] = (uint16_t)k;
         }
-    }
+    };
+    if (!SPLIT && live) write_contacts();
     __syncthreads();  // below, each wave syncs with itself (split groups: three barriers per substep)
+    if (SPLIT && live && helper) write_contacts();
     if (PL != PL_LDS) fill_alpha(tid, kWave);
     tick(PH_LOAD);
 
@@ -1008,13 +1016,22 @@ void step_kernel(StepArgs a) {
                 }
                 float4 f = s.frc[b], t = s.trq[b];
                 const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
-                for (uint32_t e = e0; e < e1; ++e) {
-                    const uint32_t ent = md.bjl[e];
-                    const float4 c = s.jw[ent & 0x3FFFFFFFu];
-                    if (c.w == 0.0f) continue;
-                    const f3 d = (ent & (1u << 30)) ? neg(xyz(c)) : xyz(c);
-                    if (ent & (1u << 31)) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
-                    else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
+                // The body's list entries and contributions are read four at a time (one LDS
+                // round trip each), then summed in list order.
+                for (uint32_t e = e0; e < e1; e += 4) {
+                    uint32_t ent[4];
+                    float4 c[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) ent[i] = e + i < e1 ? md.bjl[e + i] : 0u;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) c[i] = e + i < e1 ? s.jw[ent[i] & 0x3FFFFFFFu] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (c[i].w == 0.0f) continue;  // no contribution (or past the list's end)
+                        const f3 d = (ent[i] & (1u << 30)) ? neg(xyz(c[i])) : xyz(c[i]);
+                        if (ent[i] & (1u << 31)) { f.x = f.x + d.x; f.y = f.y + d.y; f.z = f.z + d.z; }
+                        else { t.x = t.x + d.x; t.y = t.y + d.y; t.z = t.z + d.z; }
+                    }
                 }
                 f3 vel = add(xyz(s.vel[b]), scale(scale(xyz(f), imi.x), a.dt));
                 vel = scale(vel, 0.999f);
