@@ -837,7 +837,11 @@ void step_kernel(StepArgs a) {
         if (j0 < Jp) p_jt = a.jtrq[(size_t)env * Jp + j0];
         if (j0 < N) p_lam = a.lam[(size_t)env * N + j0];
     }
-    if (live && do_prep) {
+    // The contact list and counts, read ahead into registers (one wave per group). A split
+    // group's helper reads them after the first barrier of the first substep instead, straight
+    // into LDS: the contact records are most of the bytes, and the helper needs them only after
+    // integration, while the solver's body reads then meet no contact traffic.
+    auto load_contacts = [&]() {
         if (sl < M) c0 = read_slot(&gc[sl]);
         if (sl + G < M) c1 = read_slot(&gc[sl + G]);
         if (sl + 2 * G < M) c2 = read_slot(&gc[sl + 2 * G]);
@@ -845,7 +849,8 @@ void step_kernel(StepArgs a) {
         count = a.counts[env];
         pcount = a.pcounts[env];
         detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
-    }
+    };
+    if (!SPLIT && live) load_contacts();
     // With the model records in HBM, the working-set reads follow the copy of the solve
     // records and the geom staging without a barrier in between, so their HBM latencies
     // overlap.
@@ -918,9 +923,7 @@ void step_kernel(StepArgs a) {
         for (uint32_t j = sl + G; j < Jp; j += G) s.jt[j] = a.jtrq[(size_t)env * Jp + j];
         for (uint32_t i = sl + G; i < N; i += G) s.lam[i] = a.lam[(size_t)env * N + i];
     }
-    // The contact list -> LDS. A split group's helper does this after the barrier: the solver
-    // does not read the list before the first barrier of the substep, so it starts on the
-    // bodies while the contact records (most of the bytes) are still arriving.
+    // The contact list -> LDS (from the registers read ahead above).
     auto write_contacts = [&]() {
         if (sl < M) { write_slot(&s.con[sl], c0); s.perm[sl] = (uint16_t)sl; }
         if (sl + G < M) { write_slot(&s.con[sl + G], c1); s.perm[sl + G] = (uint16_t)(sl + G); }
@@ -934,13 +937,14 @@ void step_kernel(StepArgs a) {
     };
     if (!SPLIT && live) write_contacts();
     __syncthreads();  // below, each wave syncs with itself (split groups: three barriers per substep)
-    if (SPLIT && live && helper) write_contacts();
     if (PL != PL_LDS) fill_alpha(tid, kWave);
     tick(PH_LOAD);
 
     for (uint32_t step = 0; step < a.substeps; ++step) {
         // ---- Previous-contact snapshot (cache_contacts of the last substep) -----------
-        if (live && do_prep) {
+        // A split group's helper takes it after the first barrier of the substep (with the
+        // contact list's LDS copy in the first substep), so the solver never waits for it.
+        auto snapshot = [&]() {
             const uint32_t pn = pcount < M ? pcount : M;
             const bool from_det = step == 0 && detached;
             for (uint32_t k = sl; k < pn; k += G) {
@@ -949,7 +953,8 @@ void step_kernel(StepArgs a) {
                 s.pimp[k] = make_float4(r->impulses[0], r->impulses[1], r->impulses[2],
                                         __uint_as_float(pair_key(r->indices[0], r->indices[1])));
             }
-        }
+        };
+        if (!SPLIT && live) snapshot();
         // ---- A + B: warm_start_constraints, apply_actions (:1408-1426, :196-229), then per
         // body compute_forces and update_kinematic in dispatch order (:345-388, :304-339,
         // world.zig:962-990: the torque reads the quaternion before a kinematic body's
@@ -1051,7 +1056,22 @@ void step_kernel(StepArgs a) {
         }
         wave_sync<HBM>();
         tick(PH_FORCES);
-        if (SPLIT) __syncthreads();  // split barrier 1: poses after integration are in place
+        if (SPLIT) {
+            __syncthreads();  // split barrier 1: poses after integration are in place
+            if (live && helper) {
+                if (step == 0) {
+                    count = a.counts[env];
+                    pcount = a.pcounts[env];
+                    detached = a.prev_detached != nullptr && a.prev_detached[env] != 0;
+#pragma unroll 4
+                    for (uint32_t k = sl; k < M; k += G) {
+                        write_slot(&s.con[k], read_slot(&gc[k]));
+                        s.perm[k] = (uint16_t)k;
+                    }
+                }
+                snapshot();
+            }
+        }
         // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
         // Broad phase to contact levels: the helper's part of a split group, on the poses
         // after integration (the force and torque arrays hold them; the level masks overwrite
