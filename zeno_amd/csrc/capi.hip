@@ -437,8 +437,7 @@ int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_has
 
 int zeno_amd_world_set_extended_contacts(ZenoWorldHandle world, int enable) {
     if (!world) return ZENO_INVALID_HANDLE;
-    W(world)->release_graph();
-    W(world)->ext_contacts = enable != 0;
+    W(world)->set_extended_contacts(enable != 0);
     return ZENO_SUCCESS;
 }
 

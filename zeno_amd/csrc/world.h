@@ -34,6 +34,11 @@ struct World {
     int epw = 1;
     int waves = 1;  // environment groups (waves) per workgroup (model records in LDS: one copy per workgroup)
     bool split = false;  // two waves per group: the solver and the helper (step_kernel SPLIT)
+    // The launch shape chosen at creation (extended-contact mode may switch to another one),
+    // whether a ZENO_AMD_* variable forced it, and the device's CU count.
+    int base_epw = 1, base_waves = 1;
+    bool base_split = false, shape_forced = false;
+    int cus = 256;
     EnvLds lds{};
     EnvLds lds_small{};  // placement 2: the arrays kept in LDS
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
@@ -128,6 +133,10 @@ struct World {
     hipError_t capture_steps(const float* d_actions, uint64_t stride_bytes, uint32_t steps, uint32_t substeps);
     hipError_t graph_launch();
     void release_graph();
+    // Extended-contact mode on or off. With the model records and working sets in LDS and
+    // a long contact list (M >= 64), the mode runs one environment per wave without split
+    // groups, the shape whose narrow phase visits the slots grouped by geom-type pair.
+    void set_extended_contacts(bool on);
 
    private:
     hipError_t launch(const float* d_act, uint32_t substeps, const uint8_t* d_step_mask);

@@ -188,6 +188,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
     hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, w->device);
+    w->cus = cus;
     // Placement 2 keeps the body slot masks in LDS when they fit, else in the HBM working set.
     EnvLds L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash, true);
     if ((size_t)L_small.bytes > lds_max)
@@ -256,6 +257,10 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     w->epw = epw;
     w->waves = best->waves;
     w->split = best->split;
+    w->base_epw = w->epw;
+    w->base_waves = w->waves;
+    w->base_split = w->split;
+    w->shape_forced = force_pl >= 0 || force_epw > 0 || force_waves > 0 || force_split >= 0;
 
     if ((e = hipStreamCreateWithFlags(&w->stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
     if ((e = hipStreamCreateWithFlags(&w->view_stream, hipStreamNonBlocking)) != hipSuccess) return fail("hipStreamCreate", e);
@@ -480,6 +485,31 @@ hipError_t World::step(const float* actions, uint32_t substeps, bool actions_on_
     ZA_TRY(launch(d_act, actual, nullptr));
     if (staged) ZA_TRY(mark_actions_used());
     return refresh_views();
+}
+
+void World::set_extended_contacts(bool on) {
+    release_graph();
+    ext_contacts = on;
+    if (shape_forced || placement != PL_LDS || hash) return;
+    epw = base_epw;
+    waves = base_waves;
+    split = base_split;
+    if (!on || M < 64) return;
+    // The grouped narrow phase runs in the one-environment-per-wave instances without split
+    // groups: the best of those by resident environments (the creation-time score).
+    uint64_t best = 0;
+    for (int w : {4, 1, 2}) {
+        const size_t shmem = (size_t)ml.bytes + (size_t)lds.bytes * (size_t)w;
+        const int n = resident_workgroups(1, PL_LDS, false, shmem, w, false);
+        if (n <= 0) continue;
+        const uint64_t score = std::min<uint64_t>(E, (uint64_t)n * (uint64_t)w * (uint64_t)cus);
+        if (score > best) {
+            best = score;
+            epw = 1;
+            waves = w;
+            split = false;
+        }
+    }
 }
 
 void World::release_graph() {
