@@ -105,8 +105,8 @@ def cpu_baseline(model, state, acts, num_envs: int, budget_s: float, workload: s
     }
 
 
-# The reference's published step numbers (README.md:56-59,
-# docs/reference/performance.md:13-16): 1024 envs x 1000 steps on an Apple M4 Pro.
+# The reference's published step numbers (README.md:56-59, docs/reference/performance.md:13-16
+# of the reference): 1024 envs x 1000 steps on an Apple M4 Pro.
 PUBLISHED = {"pendulum": 4.97e6, "cartpole": 6.52e6, "ant": 5.89e6, "humanoid": 5.95e6}
 
 
@@ -224,15 +224,18 @@ def bench_collide(n: int, steps: int, warmup: int, cpu_seconds: float, no_cpu: b
 
 
 def settle_steps(w, acts, limit: int = 64) -> int:
-    """Untimed steps after a reset until every env's contact list is full (the count never
-    resets, ledger Q1, so the list saturates at max_contacts within a few steps and the step
-    then does the same work every call); scenes whose counts stop growing stop early.
+    """Untimed steps after a reset until every env's contact list is full (the reference
+    never clears the count between steps, all_shaders.metal:765-766, so the list saturates at
+    max_contacts within a few steps and the step then does the same work every call); scenes
+    whose counts stop growing stop early.
     Returns the number of steps taken (actions acts[0..n))."""
     M = w.max_contacts_per_env
     prev = None
     for k in range(limit):
-        counts = w.get_prev_contact_counts()  # a copy: hands out no view
-        if counts.min() >= M or (prev is not None and np.array_equal(counts, prev)):
+        # The previous count (a copy: hands out no view) equals the current one once a step
+        # has run since the reset, which zeroed the current counts but not the previous ones.
+        counts = w.get_prev_contact_counts() if k > 0 else None
+        if counts is not None and (counts.min() >= M or (prev is not None and np.array_equal(counts, prev))):
             return k
         prev = counts
         w.step(acts[k])

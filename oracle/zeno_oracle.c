@@ -7,6 +7,13 @@
  * (src/world/world.zig:934-1293). Build with -ffp-contract=off and without fast-math.
  *
  * Parity status of each function (how it is pinned) is listed in tests/test_oracle.py.
+ *
+ * Where the reference runs unordered atomics or races, this oracle fixes one sequential
+ * schedule (the HIP kernel reproduces the same):
+ *   S1 broad-phase appends in (g, g') order;
+ *   S2 per-body joint-force sums in ascending joint order, body_a before body_b;
+ *   S3 joint constraints per colour, in colour-sorted template order;
+ *   S4 contact slots Gauss-Seidel in slot order, each slot seeing earlier slots' writes.
  */
 #include "zeno_oracle.h"
 

@@ -2,7 +2,8 @@
 
 Pinned by the closed-form fixtures in tests/golden/model_fixtures.json (C1-C4), the
 reference's own parser and decomposition tests (test_mjcf.zig, test_physics_integration.zig)
-restated as MJCF inputs, and the parser quirks the step depends on (ledger Q3, Q15, Q19).
+restated as MJCF inputs, and the parser quirks the step depends on (parser.zig:425-432,
+851, 910-975, 1229-1243, 1340-1342; world.zig:323, 397-429).
 """
 import json
 from pathlib import Path
@@ -172,7 +173,7 @@ def test_mjcf_mass_kats():
 
 
 def test_parser_layout_quirks():
-    """Ledger Q19: body positions add without rotating; joint anchor_parent = body.pos +
+    """Parser quirks (parser.zig:425-427, 910-975, 1340-1342): body positions add without rotating; joint anchor_parent = body.pos +
     joint.pos; quaternions are stored xyzw; the joint axis is not normalised; worldbody
     geoms belong to body 0; geom defaults contype = conaffinity = 1, friction[0] used."""
     xml = """<mujoco><worldbody><geom type="plane" size="1 1 0.1" friction="0.7 0.1 0.1"/>

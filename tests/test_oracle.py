@@ -117,7 +117,7 @@ def test_contact_solve_closed_form():
 
 
 def test_duplicate_slots_multiply_correction():
-    """Ledger Q1: the count is never reset, so the plane pair is appended every step and the
+    """The count is never reset between steps (all_shaders.metal:765-766), so the plane pair is appended every step and the
     sorted list holds k copies after k steps; each copy re-applies the correction."""
     m = load_model(mjcf_string=FREE_SPHERE.format(z=0.09))
     w = O.OracleWorld(m, 1)
