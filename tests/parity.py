@@ -51,9 +51,20 @@ def live_mask(counts: np.ndarray, M: int) -> np.ndarray:
     return np.arange(M)[None, :] < np.minimum(counts, M)[:, None]
 
 
-def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, atol: float) -> Dict[str, float]:
-    """Discrete outputs must match exactly; float outputs within rtol/atol. Returns the max
-    absolute difference per field (0.0 when bitwise equal) and raises on a violation."""
+def _same_bits(a: np.ndarray, b: np.ndarray, what: str) -> None:
+    """fp32 arrays equal bit for bit (signed zeros and NaN payloads included)."""
+    a32 = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    b32 = np.ascontiguousarray(b, dtype=np.float32).view(np.uint32)
+    bad = np.argwhere(a32 != b32)
+    assert bad.size == 0, f"{what}: {len(bad)} values differ in their bits, first at {tuple(bad[0])}"
+
+
+def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, atol: float,
+            exact: bool = True) -> Dict[str, float]:
+    """Discrete outputs must match exactly; float outputs within rtol/atol (the tolerances the
+    parity contract states) and, with exact, bit for bit as well (the GPU and the oracle
+    evaluate the same fp32 operations in the same order). Returns the max absolute difference
+    per field and raises on a violation."""
     out: Dict[str, float] = {}
     np.testing.assert_array_equal(g["contact_counts"], o["contact_counts"], err_msg="contact_counts")
     np.testing.assert_array_equal(g["prev_contact_counts"], o["prev_contact_counts"], err_msg="prev_contact_counts")
@@ -67,11 +78,15 @@ def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, ato
     for f in ("position_pen", "normal_friction", "impulses"):
         a, b = g["contacts"][f][live], o["contacts"][f][live]
         np.testing.assert_allclose(a, b, rtol=rtol, atol=atol, err_msg=f"contacts.{f}")
+        if exact:
+            _same_bits(a, b, f"contacts.{f}")
         out[f"contacts.{f}"] = float(np.max(np.abs(a - b))) if a.size else 0.0
     for f in FLOAT_FIELDS + ("lambda",):
         a, b = np.asarray(g[f], np.float32), np.asarray(o[f], np.float32)
         assert a.shape == b.shape, (f, a.shape, b.shape)
         np.testing.assert_allclose(a, b, rtol=rtol, atol=atol, err_msg=f)
+        if exact:
+            _same_bits(a, b, f)
         out[f] = float(np.max(np.abs(a - b))) if a.size else 0.0
     return out
 
