@@ -52,11 +52,15 @@ def live_mask(counts: np.ndarray, M: int) -> np.ndarray:
 
 
 def _same_bits(a: np.ndarray, b: np.ndarray, what: str) -> None:
-    """fp32 arrays equal bit for bit (signed zeros and NaN payloads included)."""
-    a32 = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
-    b32 = np.ascontiguousarray(b, dtype=np.float32).view(np.uint32)
-    bad = np.argwhere(a32 != b32)
-    assert bad.size == 0, f"{what}: {len(bad)} values differ in their bits, first at {tuple(bad[0])}"
+    """fp32 arrays equal bit for bit, signed zeros included. A NaN matches any NaN: IEEE 754
+    leaves the payload an operation returns to the implementation (the GPU returns the
+    canonical quiet NaN, x86 propagates an operand's)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    differ = (a.view(np.uint32) != b.view(np.uint32)) & ~(np.isnan(a) & np.isnan(b))
+    bad = np.argwhere(differ)
+    assert bad.size == 0, (f"{what}: {len(bad)} values differ in their bits, first at {tuple(bad[0])}: "
+                           f"{a[tuple(bad[0])]!r} vs {b[tuple(bad[0])]!r}")
 
 
 def compare(g: Dict[str, np.ndarray], o: Dict[str, np.ndarray], rtol: float, atol: float,
