@@ -58,3 +58,27 @@ def test_contact_list_beyond_lds_is_rejected():
     g.step(acts[0])
     o.step(acts[0])
     compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+
+
+def test_extended_mode_switches_to_the_grouped_shape_and_back():
+    """A placement-0 world with a long contact list runs the extended mode in the
+    one-environment-per-wave shape without split groups (the type-grouped narrow phase) and
+    returns to its creation-time shape when the mode is turned off; both stay on the oracle."""
+    g, o, acts = make_pair("pile", 24, 6, seed=8, max_contacts=512)
+    if g.modes()["placement"] != 0:
+        pytest.skip("the world placed this scene outside LDS")
+    base = (g.launch_config()[0], g.waves_per_group(), g.split_groups())
+    g.set_extended_contacts(True)
+    o.extended_contacts = True
+    assert g.launch_config()[0] == 1 and not g.split_groups()
+    for k in range(3):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    g.set_extended_contacts(False)
+    o.extended_contacts = False
+    assert (g.launch_config()[0], g.waves_per_group(), g.split_groups()) == base
+    for k in range(3, 6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
