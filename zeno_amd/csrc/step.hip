@@ -1,9 +1,12 @@
 // Fused physics step for CDNA4 (gfx950).
 //
-// One single-wave workgroup steps EPW environments; each environment owns G = 64 / EPW
-// lanes and an LDS working set (bodies, joint state, lambdas, the contact list and the
-// previous-contact snapshot). A launch runs every substep of one zeno_world_step call, so
-// HBM is read once and written once per call while all solver iterations stay in LDS.
+// One wave steps EPW environments; each environment owns G = 64 / EPW lanes and an LDS
+// working set (bodies, joint state, lambdas, the contact list and the previous-contact
+// snapshot). A workgroup holds up to four such groups sharing one LDS copy of the model
+// records, and in the split shapes each group has a second wave that runs the contact
+// pipeline while the first solves the joints (see step_kernel). A launch runs every substep
+// of one zeno_world_step call, so HBM is read once and written once per call while all
+// solver iterations stay in LDS.
 //
 // Stage order and arithmetic follow World.stepOnce (src/world/world.zig:934-1293) and the
 // MSL kernels of src/shaders/all_shaders.metal, cited per stage. Where the reference runs
