@@ -308,11 +308,11 @@ def main() -> int:
     # Timed region (value): the reference's own method, bench_full_physics.zig:67-83: K
     # zeno_world_step calls on host actions (the kernel reads them in place from a pinned
     # ring), wall clock between two stream synchronisations. HIP events on the world's
-    # stream around every 8th launch (every K/10-th in short runs, so that at least ten
-    # launches are timed) give the step kernel's average duration (an event pair costs a few
-    # us, so timing every launch would slow the loop it measures).
+    # stream around every 8th launch give the step kernel's average duration (an event pair
+    # costs a few us of queue time, so timing every launch, or every second one, slows the
+    # loop it measures: 70.5 -> 73.8 us per step at K = 20 when every second launch was timed).
     w.synchronize()
-    w.set_kernel_timing(True, every=max(1, min(8, args.steps // 10)))
+    w.set_kernel_timing(True, every=8)
     w.synchronize()
     t0 = time.perf_counter()
     for k in range(args.steps):
