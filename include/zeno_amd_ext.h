@@ -196,6 +196,14 @@ int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const Zeno
  * device and waits. */
 int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t n);
 
+/* No counterpart in the reference: a self-check of the device arithmetic the step relies on.
+ * y[i] = sqrt(x[i]) evaluated the way the step kernel takes the square roots it compares
+ * against a threshold (v_sqrt_f32 and the one-ulp correction, without the scaling of inputs
+ * below 2^-96), which must give the bits of the IEEE fp32 square root for every x >= 2^-96
+ * and for +-0, +inf, NaN and negative x, and a value below 2^-47 for 0 < x < 2^-96. Host
+ * arrays; runs on the current device and waits. */
+int zeno_amd_selfcheck_sqrt(const float* x, float* y, uint32_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -518,4 +518,10 @@ int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t
     return hip_status(za::selfcheck_divide_host(a, b, q, n), "selfcheck_divide");
 }
 
+int zeno_amd_selfcheck_sqrt(const float* x, float* y, uint32_t n) {
+    if (n == 0) return ZENO_SUCCESS;
+    if (!x || !y) return ZENO_INVALID_ARGUMENT;
+    return hip_status(za::selfcheck_sqrt_host(x, y, n), "selfcheck_sqrt");
+}
+
 }  // extern "C"

@@ -174,7 +174,28 @@ __global__ __launch_bounds__(256) void selfcheck_divide_kernel(const float* a, c
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) q[i] = div_r(a[i], rcp64(b[i]));
 }
+__global__ __launch_bounds__(256) void selfcheck_sqrt_kernel(const float* x, float* y, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = sqrt_gate(x[i]);
+}
 }  // namespace
+
+hipError_t selfcheck_sqrt_host(const float* x, float* y, uint32_t n) {
+    if (n == 0) return hipSuccess;
+    const size_t bytes = (size_t)n * sizeof(float);
+    float *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipMalloc(&dx, bytes);
+    if (e == hipSuccess) e = hipMalloc(&dy, bytes);
+    if (e == hipSuccess) e = hipMemcpy(dx, x, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(selfcheck_sqrt_kernel, dim3((uint32_t)(((size_t)n + 255) / 256)), dim3(256), 0, nullptr, dx, dy, n);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(y, dy, bytes, hipMemcpyDeviceToHost);
+    if (dx) hipFree(dx);
+    if (dy) hipFree(dy);
+    return e;
+}
 
 hipError_t selfcheck_divide_host(const float* a, const float* b, float* q, uint32_t n) {
     if (n == 0) return hipSuccess;

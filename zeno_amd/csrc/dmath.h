@@ -46,6 +46,20 @@ __device__ __forceinline__ f3 divs(f3 a, float s) {
 __device__ __forceinline__ f3 neg(f3 a) { return {-a.x, -a.y, -a.z}; }
 __device__ __forceinline__ float dot(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
 __device__ __forceinline__ float len(f3 a) { return __builtin_sqrtf(dot(a, a)); }
+// Square root for a value that is compared against a threshold of at least 2^-47 before the
+// root is used: v_sqrt_f32 followed by the one-ulp correction of a correctly rounded fp32
+// square root (the residuals x - s' s for s' one ulp below and above s decide between the three
+// candidates), without the scaling of inputs below 2^-96 and the final select for 0 and
+// infinity. For x >= 2^-96 the operations are those of the correctly rounded root; +-0, +inf,
+// NaN and negative x come out as the correctly rounded root does (the failing compares keep
+// s); for 0 < x < 2^-96 the result is below 2^-47 and fails every such threshold.
+__device__ __forceinline__ float sqrt_gate(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float sd = __int_as_float(__float_as_int(s) - 1), su = __int_as_float(__float_as_int(s) + 1);
+    const float t = __builtin_fmaf(-sd, s, x) <= 0.0f ? sd : s;
+    return __builtin_fmaf(-su, s, x) > 0.0f ? su : t;
+}
+__device__ __forceinline__ float len_gate(f3 a) { return sqrt_gate(dot(a, a)); }
 __device__ __forceinline__ f3 cross(f3 a, f3 b) {
     return {a.y * b.z - a.z * b.y, a.z * b.x - a.x * b.z, a.x * b.y - a.y * b.x};
 }
@@ -81,6 +95,14 @@ __device__ __forceinline__ q4 qnormalize(q4 q) {
     if (!(l > 1e-8f)) return q4{0.0f, 0.0f, 0.0f, 1.0f};
     const double y = rcp64(l);  // q / l with one reciprocal (see divs)
     return q4{div_r(q.x, y), div_r(q.y, y), div_r(q.z, y), div_r(q.w, y)};
+}
+// qnormalize with the quotients evaluated before the length test and the identity selected
+// after it (same results; sqrt_gate is exact wherever the test l > 1e-8 passes).
+__device__ __forceinline__ q4 qnormalize_sel(q4 q) {
+    const float l = sqrt_gate(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
+    const double y = rcp64(l);
+    const q4 r{div_r(q.x, y), div_r(q.y, y), div_r(q.z, y), div_r(q.w, y)};
+    return l > 1e-8f ? r : q4{0.0f, 0.0f, 0.0f, 1.0f};
 }
 // Quaternion step q + s * ((d, 0) (x) q) used by every XPBD rotation update.
 __device__ __forceinline__ q4 qdelta(f3 d, q4 q) { return qscale(qmul(mk4(d.x, d.y, d.z, 0.0f), q), 0.5f); }

@@ -210,7 +210,18 @@ __device__ __forceinline__ JState load_jstate(const JHalf& h, const Lds& s, bool
     return JState{s.pos[me], s.quat[me], s.lam[fbits(h.h0.z)]};
 }
 
-// :934-1037 positional (point-to-point), lane pair.
+// Late selects. The positional and hinge solves evaluate their update unconditionally and
+// apply the reference's conditions (C > 1e-6, w > 1e-8, inverse mass > 0) only to the values
+// they store: a compare that feeds a branch or a select right away waits about 30 cycles for
+// its lane mask, while one whose mask is needed only at the stores overlaps the rest of the
+// solve. A store that the reference skips writes back the value the lane read, so the memory
+// is unchanged (the constraints of one phase touch disjoint bodies; a static body that several
+// constraints share only ever gets its own value written back). The square roots compared
+// against those thresholds use sqrt_gate, which is the correctly rounded root wherever the
+// comparison can pass.
+
+// :934-1037 positional (point-to-point), lane pair. r - qrot(com, q) is evaluated for every
+// centre of mass: for com = +0 and a finite q the rotated offset is exactly +0 and r - (+0) == r.
 __device__ __forceinline__ void solve_positional2(const JHalf& h, const JState& st, const Lds& s, bool odd) {
     const uint32_t ia = fbits(h.h0.x), ib = fbits(h.h0.y), ci = fbits(h.h0.z);
     const uint32_t me = odd ? ib : ia;
@@ -224,28 +235,20 @@ __device__ __forceinline__ void solve_positional2(const JHalf& h, const JState& 
     const f3 rr = qrot(xyz(h.v1), Q);                      // r_a or r_b
     const f3 u = add(P, rr);                               // pos + r
     const f3 diff = sub(pair_a(u), pair_b(u));             // (pos_a + r_a) - (pos_b + r_b)
-    const float C = len(diff);
-    if (C > 1e-6f) {
-        const f3 n = divs(diff, C);
-        const f3 rn = cross(rr, n);
-        const float t = inv_mass + dot(mul(rn, iI), rn);
-        const float w = t + pair_swap(t);                  // (w_a) + (w_b), addition commutes
-        const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
-        s.lam[ci] = lambda_prev + d_lambda;  // both lanes store the same value
-        const f3 impulse = sscale(d_lambda, n);
-        // r - qrot(com, q): with com = +0 and a finite q the rotated offset is exactly +0 and
-        // r - (+0) = r, so the rotation is skipped. A finite sum of the components implies
-        // four finite components (an infinite or NaN one makes the sum infinite or NaN); a
-        // finite q whose sum overflows just takes the rotation.
-        const bool com_zero = ((fbits(h.h0.w) >> (odd ? 3 : 2)) & 1u) != 0 &&
-                              __builtin_isfinite((Q.x + Q.y) + (Q.z + Q.w));
-        f3 rc = rr;
-        if (!com_zero) rc = sub(rr, qrot(xyz(h.v2), Q));
-        if (inv_mass > 0) {
-            set_xyz(&s.pos[me], add(P, scale(impulse, sg * inv_mass)));
-            s.quat[me] = tof4(qnormalize(qadd(Q, qdelta_signed(mul(cross(rc, impulse), iI), Q, sg))));
-        }
-    }
+    const float C = len_gate(diff);
+    const f3 n = divs(diff, C);
+    const f3 rn = cross(rr, n);
+    const float t = inv_mass + dot(mul(rn, iI), rn);
+    const float w = t + pair_swap(t);                      // (w_a) + (w_b), addition commutes
+    const float d_lambda = (-C - alpha_tilde * lambda_prev) / (w + alpha_tilde);
+    const f3 impulse = sscale(d_lambda, n);
+    const f3 rc = sub(rr, qrot(xyz(h.v2), Q));
+    const f3 Pn = add(P, scale(impulse, sg * inv_mass));
+    const q4 Qn = qnormalize_sel(qadd(Q, qdelta_signed(mul(cross(rc, impulse), iI), Q, sg)));
+    const bool act = C > 1e-6f, moved = act && inv_mass > 0;
+    s.lam[ci] = act ? lambda_prev + d_lambda : lambda_prev;  // both lanes store the same value
+    set_xyz(&s.pos[me], moved ? Pn : P);
+    s.quat[me] = tof4(moved ? Qn : Q);
 }
 
 // :1131-1186 hinge axis alignment, lane pair.
@@ -257,18 +260,16 @@ __device__ __forceinline__ void solve_angular2(const JHalf& h, const JState& st,
     const q4 Q = toq(st.Q);
     const f3 axw = qrot(xyz(h.v1), Q);
     const f3 cr = cross(pair_a(axw), pair_b(axw));
-    const float sin_angle = len(cr);
-    if (sin_angle > 1e-6f) {
-        const f3 n = divs(cr, sin_angle);
-        const float ang_C = z_asinf(clampf(sin_angle, -1.0f, 1.0f));
-        const float t = dot(mul(n, iI), n);
-        const float w = t + pair_swap(t);
-        if (w > 1e-8f) {
-            const float d_lambda = -ang_C / (w + alpha_tilde);
-            const float dl = odd ? -d_lambda : d_lambda;
-            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, qdelta(mul(sscale(dl, n), iI), Q))));
-        }
-    }
+    const float sin_angle = len_gate(cr);
+    const f3 n = divs(cr, sin_angle);
+    const float ang_C = z_asinf(clampf(sin_angle, -1.0f, 1.0f));
+    const float t = dot(mul(n, iI), n);
+    const float w = t + pair_swap(t);
+    const float d_lambda = -ang_C / (w + alpha_tilde);
+    const float dl = odd ? -d_lambda : d_lambda;
+    const q4 Qn = qnormalize_sel(qadd(Q, qdelta(mul(sscale(dl, n), iI), Q)));
+    const bool moved = sin_angle > 1e-6f && w > 1e-8f && inv_mass > 0;
+    s.quat[me] = tof4(moved ? Qn : Q);
 }
 
 // :1189-1238 angular limit, lane pair.
@@ -291,11 +292,12 @@ __device__ __forceinline__ void solve_angular_limit2(const JHalf& h, const JStat
         const f3 aw = qrot(axis_local, qa);
         const float t = dot(mul(aw, iI), aw);
         const float w = t + pair_swap(t);
-        if (w > 1e-8f) {
-            const float d_lambda = violation / (w + alpha_tilde);
-            const f3 ang_impulse = sscale(d_lambda, aw);
-            if (inv_mass > 0) s.quat[me] = tof4(qnormalize(qadd(Q, qdelta_signed(mul(ang_impulse, iI), Q, sg))));
-        }
+        // Inside the violation branch (the common case is no violation, which skips the
+        // update): the update is evaluated before its conditions, as above.
+        const float d_lambda = violation / (w + alpha_tilde);
+        const f3 ang_impulse = sscale(d_lambda, aw);
+        const q4 Qn = qnormalize_sel(qadd(Q, qdelta_signed(mul(ang_impulse, iI), Q, sg)));
+        if (w > 1e-8f && inv_mass > 0) s.quat[me] = tof4(Qn);
     }
 }
 
@@ -501,7 +503,7 @@ __device__ __forceinline__ void solve_contact_rec(const Mdl& md, const Lds& s, c
     const f3 rel_vel = sub(pair_a(vpt), pair_b(vpt));
     const float vel_normal = dot(rel_vel, normal);
     const f3 vel_tangent = sub(rel_vel, sscale(vel_normal, normal));
-    const float tangent_speed = len(vel_tangent);
+    const float tangent_speed = len_gate(vel_tangent);  // used only when > 1e-6
     const f3 rn = cross(r, normal);
     const float tn = inv_mass + dot(mul(rn, iI), rn);
     const float w_normal = tn + pair_swap(tn);
