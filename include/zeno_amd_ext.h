@@ -191,7 +191,7 @@ int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const Zeno
 
 /* No counterpart in the reference: a self-check of the device arithmetic the step relies on.
  * q[i] = a[i] / b[i] evaluated the way the step kernel divides several numbers by one divisor
- * (one fp64 reciprocal from v_rcp_f64 and two Newton steps, then fp32(a * y)), which must give
+ * (one fp64 reciprocal from v_rcp_f64 and its cubic correction, then fp32(a * y)), which must give
  * the bits of the IEEE fp32 division for every input. Host arrays; runs on the current
  * device and waits. */
 int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t n);
@@ -203,6 +203,13 @@ int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t
  * and for +-0, +inf, NaN and negative x, and a value below 2^-47 for 0 < x < 2^-96. Host
  * arrays; runs on the current device and waits. */
 int zeno_amd_selfcheck_sqrt(const float* x, float* y, uint32_t n);
+
+/* No counterpart in the reference: a self-check of the device arithmetic the step relies on.
+ * *max_err = the largest |1 - b y| over every finite nonzero fp32 b, with y the fp64
+ * reciprocal the step divides by (v_rcp_f64 and its cubic correction). The quotients a * y are
+ * the correctly rounded fp32 a / b when this is below about 2^-49.1. Runs on the current
+ * device (2^32 divisors, well under a second) and waits. */
+int zeno_amd_selfcheck_reciprocal_error(double* max_err);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,5 @@
 """The step kernel divides several fp32 numbers by one divisor through one fp64 reciprocal
-(v_rcp_f64 and two Newton steps, then fp32(a * y); `rcp64` / `div_r` in dmath.h), which must
+(v_rcp_f64 and a cubic correction, then fp32(a * y); `rcp64` / `div_r` in dmath.h), which must
 give the bits of the IEEE fp32 division the reference and the oracle evaluate. The same device
 code, through zeno_amd_selfcheck_divide, against numpy's fp32 division: every significand of
 the numerator against a set of divisors (normal, subnormal, huge, negative), random bit
@@ -68,3 +68,12 @@ def test_special_values():
     a, b = np.meshgrid(vals, vals, indexing="ij")
     assert_same_bits(device_quotients(a.reshape(-1), b.reshape(-1)), ieee_quotients(a.reshape(-1), b.reshape(-1)),
                      "special")
+
+
+def test_reciprocal_error_over_every_divisor():
+    """The proof of correct rounding needs |1 - b y| below about 2^-49.1 for every divisor; the
+    device reports the maximum over all 2^32 fp32 bit patterns (finite, nonzero)."""
+    lib = _lib.load()
+    err = C.c_double(-1.0)
+    assert lib.zeno_amd_selfcheck_reciprocal_error(C.byref(err)) == 0, _lib.last_error()
+    assert 0.0 < err.value <= 2.0**-52, err.value

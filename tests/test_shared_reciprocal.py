@@ -1,10 +1,10 @@
 """The step kernel divides several fp32 numbers by one divisor through a single fp64
-reciprocal (`rcp64` / `div_r` in zeno_amd/csrc/dmath.h: y = 1/b from v_rcp_f64 and two Newton
-steps, then each quotient is fp32(fp64(a * y))). Its results must be the bits of the fp32
+reciprocal (`rcp64` / `div_r` in zeno_amd/csrc/dmath.h: y = 1/b from v_rcp_f64 and its cubic
+correction, then each quotient is fp32(fp64(a * y))). Its results must be the bits of the fp32
 division a / b that the reference and the oracle evaluate. This checks that property of the
 arithmetic on the CPU (numpy's float32 division and float64 product are IEEE, round to nearest
-even), with y off by up to 4 fp64 ulps of 1/b (two Newton steps give about one; the bound
-allows about 8), over random operands spanning the whole fp32 range including subnormals,
+even), with y off by up to 4 fp64 ulps of 1/b (the device's y is within 2^-53 relative, about
+one ulp, over every fp32 divisor; the bound allows about 8), over random operands spanning the whole fp32 range including subnormals,
 every significand of a against a set of divisors, and the special values (zeros, infinities,
 NaN), where the kernel keeps the raw reciprocal. tests/test_gpu_divide.py runs the device
 code itself over the same operands.

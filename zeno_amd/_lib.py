@@ -172,6 +172,7 @@ SIGNATURES = {
     "zeno_amd_detect_collisions_host_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p]),
     "zeno_amd_selfcheck_divide": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]),
     "zeno_amd_selfcheck_sqrt": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32]),
+    "zeno_amd_selfcheck_reciprocal_error": (C.c_int, [C.c_void_p]),
     "zeno_amd_world_waves_per_group": (C.c_uint32, [C.c_void_p]),
     "zeno_amd_world_split_groups": (C.c_int, [C.c_void_p]),
 }

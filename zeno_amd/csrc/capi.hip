@@ -524,4 +524,9 @@ int zeno_amd_selfcheck_sqrt(const float* x, float* y, uint32_t n) {
     return hip_status(za::selfcheck_sqrt_host(x, y, n), "selfcheck_sqrt");
 }
 
+int zeno_amd_selfcheck_reciprocal_error(double* max_err) {
+    if (!max_err) return ZENO_INVALID_ARGUMENT;
+    return hip_status(za::selfcheck_rcp_error_host(max_err), "selfcheck_reciprocal_error");
+}
+
 }  // extern "C"

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cstring>
 #include <mutex>
 
 #include "collide.h"
@@ -174,11 +175,41 @@ __global__ __launch_bounds__(256) void selfcheck_divide_kernel(const float* a, c
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) q[i] = div_r(a[i], rcp64(b[i]));
 }
+// max |1 - b rcp64(b)| over the fp32 bit patterns [base, base + 2^32 / gridDim.x ...): each
+// thread takes 256 consecutive patterns; a wave reduces its lanes and one lane folds the wave's
+// maximum into *out with a vector atomic (non-negative doubles order as their bit patterns).
+__global__ __launch_bounds__(256) void selfcheck_rcp_error_kernel(unsigned long long* out) {
+    const uint64_t base = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 256ull;
+    double m = 0.0;
+    for (uint32_t i = 0; i < 256u; ++i) {
+        const float b = __uint_as_float((uint32_t)(base + i));
+        if (!__builtin_isfinite(b) || b == 0.0f) continue;
+        m = fmax(m, __builtin_fabs(__builtin_fma(-(double)b, rcp64(b), 1.0)));
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmax(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63u) == 0u) atomicMax(out, (unsigned long long)__double_as_longlong(m));
+}
 __global__ __launch_bounds__(256) void selfcheck_sqrt_kernel(const float* x, float* y, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = sqrt_gate(x[i]);
 }
 }  // namespace
+
+hipError_t selfcheck_rcp_error_host(double* max_err) {
+    unsigned long long* d = nullptr;
+    hipError_t e = hipMalloc(&d, sizeof *d);
+    if (e == hipSuccess) e = hipMemset(d, 0, sizeof *d);
+    if (e == hipSuccess) {
+        // 65,536 workgroups x 256 threads x 256 patterns = 2^32
+        hipLaunchKernelGGL(selfcheck_rcp_error_kernel, dim3(65536), dim3(256), 0, nullptr, d);
+        e = hipGetLastError();
+    }
+    unsigned long long bits = 0;
+    if (e == hipSuccess) e = hipMemcpy(&bits, d, sizeof bits, hipMemcpyDeviceToHost);
+    if (d) hipFree(d);
+    if (e == hipSuccess) std::memcpy(max_err, &bits, sizeof bits);
+    return e;
+}
 
 hipError_t selfcheck_sqrt_host(const float* x, float* y, uint32_t n) {
     if (n == 0) return hipSuccess;

@@ -25,8 +25,11 @@ __device__ __forceinline__ f3 sscale(float s, f3 a) { return {s * a.x, s * a.y, 
 // exact quotient a / b is either an fp32 number or at least 2^-49 (relative) away from every
 // rounding boundary of the fp32 grid: with a = A 2^ea, b = B 2^eb (A, B < 2^24) and a boundary
 // m = M 2^em (M odd, < 2^25), a - m b is a nonzero multiple of 2^(em+eb), so
-// |a / b - m| >= 2^(em+eb) / b > 2^-49 m. y = 1 / b from v_rcp_f64 refined by two Newton steps
-// is within ~2^-53 (relative) of 1 / b; a * y rounded to fp64 is then within ~2^-52 of a / b, on
+// |a / b - m| >= 2^-49 m. y = 1 / b is the v_rcp_f64 estimate r0 refined by the cubic
+// correction r0 (1 + e + e^2), e = 1 - b r0 (three dependent fp64 FMAs; the relative error
+// becomes about e^3 plus one rounding). Over every finite nonzero fp32 b, |1 - b r0| <= 2^-24.39
+// and |1 - b y| <= 2^-53 (measured exhaustively on gfx950: zeno_amd_selfcheck_reciprocal_error);
+// a * y rounded to fp64 is then within ~2^-52 of a / b, on
 // the same side of every boundary, so its rounding to fp32 is the correctly rounded a / b (the
 // bits of the fp32 division, subnormal and overflowing quotients included: the fp64 range holds
 // every fp32 quotient). A zero or infinite divisor keeps the raw reciprocal (+-inf, +-0, exact),
@@ -34,8 +37,8 @@ __device__ __forceinline__ f3 sscale(float s, f3 a) { return {s * a.x, s * a.y, 
 __device__ __forceinline__ double rcp64(float b) {
     const double d = (double)b;
     const double r0 = __builtin_amdgcn_rcp(d);
-    double r = __builtin_fma(r0, __builtin_fma(-d, r0, 1.0), r0);
-    r = __builtin_fma(r, __builtin_fma(-d, r, 1.0), r);
+    const double e = __builtin_fma(-d, r0, 1.0);
+    const double r = __builtin_fma(r0, __builtin_fma(e, e, e), r0);
     return (__builtin_isfinite(b) && b != 0.0f) ? r : r0;
 }
 __device__ __forceinline__ float div_r(float a, double y) { return (float)((double)a * y); }
