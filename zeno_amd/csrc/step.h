@@ -143,8 +143,7 @@ constexpr uint32_t kJHalfQuads = 4;  // float4 per lane-pair half record
 struct JointPhase { uint32_t type, start, count, pad; };
 
 // Record layout (float4 quads). q0 = (ia, ib, template index, flags) [u32]; flags: bit0
-// inv_m_a > 0, bit1 inv_m_b > 0, bit2 / bit3 the centre of mass of body a / b is exactly
-// +0, bits 8-15 the constraint type.
+// inv_m_a > 0, bit1 inv_m_b > 0, bits 8-15 the constraint type.
 // Lane-pair types (POSITIONAL, ANGULAR, ANGULAR_LIMIT) hold two halves, quads 0-3 for the
 // lane of body a and quads 4-7 for the lane of body b, each laid out as
 //   h0 = q0,  h1 = inverse mass and inertia of the lane's body,
@@ -184,14 +183,7 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
                 if (ma[0] + mb[0] < 1e-8f) continue;  // all_shaders.metal:924: nothing to move
                 float4 q[kJRecQuads];
                 for (auto& x : q) x = make_float4(0, 0, 0, 0);
-                auto pos_zero = [](const float* v) {  // all three components +0.0f
-                    uint32_t b[3];
-                    std::memcpy(b, v, 12);
-                    return (b[0] | b[1] | b[2]) == 0u;
-                };
-                const uint32_t flags = (ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u) |
-                                       (pos_zero(com + 4 * ia) ? 4u : 0u) | (pos_zero(com + 4 * ib) ? 8u : 0u) |
-                                       (type << 8);
+                const uint32_t flags = (ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u) | (type << 8);
                 const float4 head = make_float4(u(ia), u(ib), u(k), u(flags));
                 const float4 mia = make_float4(ma[0], ma[1], ma[2], ma[3]);
                 const float4 mib = make_float4(mb[0], mb[1], mb[2], mb[3]);
