@@ -88,6 +88,10 @@ int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, ui
 
 /* Launch configuration chosen for the world: environments per wavefront and LDS bytes
  * per workgroup (with the working sets in HBM, the contact and hash arrays kept in LDS). */
+/* No counterpart in the reference: the number of joint-solve phases per solver iteration
+ * (same-type runs of one colour, after the constraints that can never act are left out: those
+ * with nothing to move and angular limits whose bounds lie beyond +-2 pi). 0 for NULL. */
+uint32_t zeno_amd_world_joint_phases(ZenoWorldHandle world);
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes);
 
 /* Environment groups per workgroup of the world's step launches (1..4; with the model records

@@ -160,6 +160,7 @@ SIGNATURES = {
     "zeno_amd_world_synchronize": (C.c_int, [_vp]),
     "zeno_amd_world_set_kernel_timing": (C.c_int, [_vp, C.c_int]),
     "zeno_amd_world_get_kernel_timing": (C.c_int, [_vp, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
+    "zeno_amd_world_joint_phases": (C.c_uint32, [C.c_void_p]),
     "zeno_amd_world_launch_config": (C.c_int, [_vp, _u32p, _u32p]),
     "zeno_amd_world_modes": (C.c_int, [_vp, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "zeno_amd_world_get_cell_ids": (C.c_int, [_vp, _u32p]),

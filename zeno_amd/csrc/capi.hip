@@ -414,6 +414,11 @@ int zeno_amd_world_get_kernel_timing(ZenoWorldHandle world, double* total_ms, ui
     return hip_status(W(world)->kernel_timing(total_ms, launches), "get_kernel_timing");
 }
 
+uint32_t zeno_amd_world_joint_phases(ZenoWorldHandle world) {
+    if (!world) return 0;
+    return W(world)->njph;
+}
+
 int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave, uint32_t* lds_bytes) {
     if (!world) return ZENO_INVALID_HANDLE;
     const World* w = W(world);

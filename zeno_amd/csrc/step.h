@@ -138,6 +138,7 @@ inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G
 // order inside the colour, and every phase takes one branch for the whole wave.
 // Templates that the solver skips (types without a solver, or two static bodies) are
 // dropped here.
+constexpr float kTwoPiF = 6.28318548f;  // 2 * fp32(pi), the largest |2 atan2(y, x)|
 constexpr uint32_t kJRecQuads = 8;  // float4 per solve record
 constexpr uint32_t kJHalfQuads = 4;  // float4 per lane-pair half record
 struct JointPhase { uint32_t type, start, count, pad; };
@@ -181,6 +182,13 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
                 const float* ma = invmi + 4 * ia;
                 const float* mb = invmi + 4 * ib;
                 if (ma[0] + mb[0] < 1e-8f) continue;  // all_shaders.metal:924: nothing to move
+                // An angular limit whose bounds lie beyond +-2 pi can never act: its angle
+                // 2 atan2(...) (:1206) is within +-6.28318548 for every input (atan2 returns at
+                // most fp32(pi) = 3.14159274 in magnitude), so neither angle < lower nor
+                // angle > upper holds (NaN compares false as well), the violation stays 0 and
+                // the solve writes nothing (:1216). Such bounds are MJCF ranges in degrees, which
+                // the reference's parser keeps as given (ant.xml's hips: -30..30).
+                if (type == C_ANGULAR_LIMIT && t.limits[0] <= -kTwoPiF && t.limits[1] >= kTwoPiF) continue;
                 float4 q[kJRecQuads];
                 for (auto& x : q) x = make_float4(0, 0, 0, 0);
                 const uint32_t flags = (ma[0] > 0 ? 1u : 0u) | (mb[0] > 0 ? 2u : 0u) | (type << 8);

@@ -395,6 +395,11 @@ class ZenoWorld:
             raise RuntimeError(f"get_kernel_timing failed: {rc}")
         return ms.value, n.value
 
+    def joint_phases(self) -> int:
+        """Joint-solve phases per solver iteration (same-type runs of one colour), after the
+        constraints that can never act are left out."""
+        return int(self._lib.zeno_amd_world_joint_phases(self._handle))
+
     def launch_config(self) -> Tuple[int, int]:
         epw = C.c_uint32()
         lds = C.c_uint32()
