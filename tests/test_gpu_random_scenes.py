@@ -24,10 +24,29 @@ pytestmark = pytest.mark.gpu
 TOL = dict(rtol=1e-5, atol=1e-6)
 
 
-def random_scene_mjcf(rng: np.random.Generator) -> str:
+def _mixed_range(rng: np.random.Generator) -> str:
+    """A joint range of one of the kinds the assets carry: none, small in radians, MJCF degrees
+    on both sides (bounds beyond +-2 pi: an angular limit that can never act), degrees on one
+    side (a hinge limit the angle is always beyond), or bounds at the +-2 pi threshold itself."""
+    kind = rng.choice(["none", "radians", "degrees", "one_sided", "threshold"], p=[0.2, 0.2, 0.3, 0.1, 0.2])
+    if kind == "none":
+        return ""
+    if kind == "radians":
+        lo, hi = rng.uniform(-1.2, -0.1), rng.uniform(0.1, 1.2)
+    elif kind == "degrees":
+        lo, hi = -rng.uniform(10, 150), rng.uniform(10, 150)
+    elif kind == "one_sided":
+        lo, hi = -rng.uniform(60, 150), -rng.uniform(10, 50)
+    else:
+        b = 6.2832 if rng.random() < 0.5 else 6.2831  # float32: just beyond / just inside 2 fp32(pi)
+        lo, hi = -b, b
+    return f' range="{lo:.4f} {hi:.4f}"'
+
+
+def random_scene_mjcf(rng: np.random.Generator, ranges: str = "small") -> str:
     """An articulated scene over a ground plane: 1-3 trees up to depth 3, each body with one
     joint (or none: an implicit fixed joint) and one geom; motors on some hinge and slide
-    joints; joint and frame sensors."""
+    joints; joint and frame sensors. ranges="mixed" draws the joint ranges from _mixed_range."""
     lines = ["<mujoco><worldbody>", '<geom type="plane" size="5 5 0.1"/>']
     joints, bodies = [], []
 
@@ -45,7 +64,10 @@ def random_scene_mjcf(rng: np.random.Generator) -> str:
         if kind != "none":
             jn = f"j{len(joints)}"
             joints.append((jn, kind))
-            rng_attr = f' range="{rng.uniform(-1.2, -0.1):.3f} {rng.uniform(0.1, 1.2):.3f}"' if rng.random() < 0.5 else ""
+            if ranges == "small":
+                rng_attr = f' range="{rng.uniform(-1.2, -0.1):.3f} {rng.uniform(0.1, 1.2):.3f}"' if rng.random() < 0.5 else ""
+            else:
+                rng_attr = _mixed_range(rng)
             ax = rng.normal(size=3)
             ax /= np.linalg.norm(ax)
             out.append(f'<joint name="{jn}" type="{kind}" axis="{" ".join(f"{v:.4f}" for v in ax)}"'
@@ -113,11 +135,7 @@ def _world(xml: str, envs: int, shape: dict) -> ZenoWorld:
 STABLE_SEEDS = [1, 2, 3, 4, 6, 8, 9]
 
 
-@pytest.mark.parametrize("shape", sorted(SHAPES))
-@pytest.mark.parametrize("seed", STABLE_SEEDS)
-def test_random_scene_matches_oracle(seed, shape):
-    rng = np.random.default_rng(1000 + seed)
-    xml = random_scene_mjcf(rng)
+def _run_scene(rng: np.random.Generator, xml: str, shape: str) -> None:
     E, steps = 13, 24  # an env count that leaves the last group partly empty
     g = _world(xml, E, SHAPES[shape])
     o = OracleWorld(load_model(mjcf_string=xml), E)
@@ -139,6 +157,32 @@ def test_random_scene_matches_oracle(seed, shape):
         compare(gpu_arrays(g), oracle_arrays(o), **TOL)
     assert np.isfinite(g.get_body_positions(zero_copy=False)).all()
     g.close()
+
+
+@pytest.mark.parametrize("shape", sorted(SHAPES))
+@pytest.mark.parametrize("seed", STABLE_SEEDS)
+def test_random_scene_matches_oracle(seed, shape):
+    rng = np.random.default_rng(1000 + seed)
+    _run_scene(rng, random_scene_mjcf(rng), shape)
+
+
+# Mixed joint ranges: seeds whose scenes stay finite over the run and hold both an angular limit
+# that can never act (bounds beyond +-2 pi, left out of the GPU's joint program while the oracle
+# evaluates it) and one that can.
+MIXED_SEEDS = [2, 5, 8, 9, 12, 14, 15, 16]
+TWO_PI_F = np.float32(6.28318548)
+
+
+@pytest.mark.parametrize("shape", ["auto", "one_env_per_wave", "split_epw4", "model_in_hbm"])
+@pytest.mark.parametrize("seed", MIXED_SEEDS)
+def test_random_scene_mixed_ranges_match_oracle(seed, shape):
+    rng = np.random.default_rng(5000 + seed)
+    xml = random_scene_mjcf(rng, ranges="mixed")
+    c = load_model(mjcf_string=xml)["constraints"]
+    lim = [k for k in range(len(c)) if (int(c[k]["indices"][3]) & 0xFF) == 4]
+    never = [k for k in lim if np.float32(c[k]["limits"][0]) <= -TWO_PI_F and np.float32(c[k]["limits"][1]) >= TWO_PI_F]
+    assert 0 < len(never) < len(lim)
+    _run_scene(rng, xml, shape)
 
 
 # In the extended-contact mode the same scenes also collide boxes and capsules with each other
