@@ -100,6 +100,27 @@ def test_zero_copy_views():
         assert C.addressof(raw.contents) == p1.ctypes.data
 
 
+def test_reused_views_are_separate_arrays_and_copies_do_not_alias():
+    """The getters build one ndarray per host mirror and hand out views of it: each zero-copy
+    call is its own array object over the mirror, each copy is fresh memory that later steps do
+    not change, and closing the world drops the arrays."""
+    with ZenoWorld(mjcf_string=PENDULUM_MJCF, num_envs=2) as w:
+        v1, v2 = w.get_body_positions(), w.get_body_positions()
+        assert v1 is not v2 and v1.ctypes.data == v2.ctypes.data
+        v1.shape = (-1,)  # reshaping one handed-out view leaves the next one alone
+        assert w.get_body_positions().shape == (2, w.num_bodies, 4)
+        o1 = w.get_observations()
+        r1, d1 = w.get_rewards(), w.get_dones()
+        for _ in range(3):
+            w.step(np.ones((2, 1), np.float32))
+        o2 = w.get_observations()
+        assert not np.shares_memory(o1, o2) and not np.array_equal(o1, o2)
+        np.testing.assert_array_equal(o2, w.get_sensor_data())
+        assert not np.shares_memory(r1, w.get_rewards()) and not np.shares_memory(d1, w.get_dones())
+        assert w._views
+    assert not w._views
+
+
 def test_held_views_follow_every_state_change():
     """Views taken once stay current across step, step_subset, reset, reset_to_state and the
     setters (the reference's shared-memory buffers do), and match the oracle after steps."""

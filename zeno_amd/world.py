@@ -60,6 +60,7 @@ class ZenoWorld:
     ):
         self._lib = L.load()
         self._handle = None
+        self._views: Dict[Any, np.ndarray] = {}
         if mjcf_path is None and mjcf_string is None:
             raise ValueError("Either mjcf_path or mjcf_string must be provided")
         cfg = L.ZenoConfig(num_envs=num_envs, timestep=timestep, contact_iterations=contact_iterations,
@@ -89,6 +90,7 @@ class ZenoWorld:
 
     def close(self) -> None:
         if self._handle:
+            self._views.clear()
             self._lib.zeno_world_destroy(self._handle)
             self._handle = None
 
@@ -200,9 +202,16 @@ class ZenoWorld:
     def _view(self, ptr, shape: Tuple[int, ...], ctype, dtype, zero_copy: bool) -> np.ndarray:
         if not ptr:
             return np.zeros(shape, dtype=dtype)
-        count = int(np.prod(shape))
-        arr = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ctype)), shape=(count,)).view(dtype).reshape(shape)
-        return arr if zero_copy else arr.copy()
+        # Each host mirror keeps one address for the world's lifetime, so its ndarray is built
+        # once (a ctypes-to-numpy view costs a few microseconds, a getter call in an RL loop
+        # is otherwise ~1 us); the C call above still runs every time and does the refresh.
+        key = (C.addressof(ptr.contents), shape, dtype)
+        arr = self._views.get(key)
+        if arr is None:
+            count = int(np.prod(shape))
+            arr = np.ctypeslib.as_array(C.cast(ptr, C.POINTER(ctype)), shape=(count,)).view(dtype).reshape(shape)
+            self._views[key] = arr
+        return arr.view() if zero_copy else arr.copy()
 
     def _body(self, fn, zero_copy: bool) -> np.ndarray:
         return self._view(fn(self._handle), (self._num_envs, self._num_bodies, 4), C.c_float, np.float32, zero_copy)
