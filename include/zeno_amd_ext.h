@@ -73,6 +73,12 @@ int zeno_amd_device_count(void);
 int zeno_amd_world_get_lambda(ZenoWorldHandle world, float* out /* [E*N] */);
 int zeno_amd_world_get_prev_contact_counts(ZenoWorldHandle world, uint32_t* out /* [E] */);
 
+/* Set every env's contact count (u32, never cleared by a step, so it wraps after 2^32
+ * appends). Replaces a caller's write through the pointer zeno_world_get_contact_counts
+ * returns, which is shared memory in the reference (src/main.zig:557-560). Copies from caller
+ * memory; held views follow; returns 0 or an error code. */
+int zeno_amd_world_set_contact_counts(ZenoWorldHandle world, const uint32_t* counts /* [E] */);
+
 /* Step with actions already in device memory (d_actions: [E*A] floats on the world's
  * device). Same semantics as zeno_world_step. */
 int zeno_amd_world_step_device(ZenoWorldHandle world, const float* d_actions, uint32_t substeps);

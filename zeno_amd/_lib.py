@@ -156,6 +156,7 @@ SIGNATURES = {
     "zeno_amd_device_count": (C.c_int, []),
     "zeno_amd_world_get_lambda": (C.c_int, [_vp, _fp]),
     "zeno_amd_world_get_prev_contact_counts": (C.c_int, [_vp, _u32p]),
+    "zeno_amd_world_set_contact_counts": (C.c_int, [_vp, _u32p]),
     "zeno_amd_world_step_device": (C.c_int, [_vp, C.c_void_p, C.c_uint32]),
     "zeno_amd_world_synchronize": (C.c_int, [_vp]),
     "zeno_amd_world_set_kernel_timing": (C.c_int, [_vp, C.c_int]),

@@ -386,6 +386,12 @@ int zeno_amd_world_get_prev_contact_counts(ZenoWorldHandle world, uint32_t* out)
     return hip_status(e, "get_prev_contact_counts");
 }
 
+int zeno_amd_world_set_contact_counts(ZenoWorldHandle world, const uint32_t* counts) {
+    if (!world) return ZENO_INVALID_HANDLE;
+    if (!counts) return ZENO_INVALID_ARGUMENT;
+    return hip_status(W(world)->set_contact_counts(counts), "set_contact_counts");
+}
+
 int zeno_amd_world_step_device(ZenoWorldHandle world, const float* d_actions, uint32_t substeps) {
     if (!world) return ZENO_INVALID_HANDLE;
     World* w = W(world);

@@ -126,6 +126,7 @@ struct World {
     // Brings every exposed mirror up to date after device work; returns once the copies are
     // done. A no-op when no mirror has been handed out.
     hipError_t refresh_views();
+    hipError_t set_contact_counts(const uint32_t* counts);
     hipError_t sync();
     hipError_t get_profiling(ZenoProfilingData* out);
     hipError_t kernel_timing(double* ms, uint64_t* launches);

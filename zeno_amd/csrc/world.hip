@@ -622,6 +622,16 @@ hipError_t World::reset(const uint8_t* mask) {
     return refresh_views();
 }
 
+// A caller's write through the contact-count pointer the reference hands out (shared memory
+// there, main.zig:557-560): the counts become the device's, and the held views follow.
+hipError_t World::set_contact_counts(const uint32_t* counts) {
+    ZA_TRY(hipSetDevice(device));
+    ZA_TRY(hipMemcpyAsync(d_counts, counts, (size_t)E * 4, hipMemcpyHostToDevice, stream));
+    ZA_TRY(hipStreamSynchronize(stream));
+    mark_all_dirty();
+    return refresh_views();
+}
+
 hipError_t World::set_state_array(float4* dst, MirrorId mid, const float* src, const uint8_t* mask) {
     ZA_TRY(write_state_array(dst, mid, src, mask));
     return refresh_views();

@@ -357,6 +357,14 @@ class ZenoWorld:
                 raise RuntimeError(f"get_lambda failed: {rc}")
         return out
 
+    def set_contact_counts(self, counts: np.ndarray) -> None:
+        c = np.ascontiguousarray(counts, dtype=np.uint32)
+        if c.shape != (self._num_envs,):
+            raise ValueError(f"counts must have shape ({self._num_envs},), got {c.shape}")
+        rc = self._lib.zeno_amd_world_set_contact_counts(self._handle, c.ctypes.data_as(C.POINTER(C.c_uint32)))
+        if rc != 0:
+            raise RuntimeError(f"set_contact_counts failed: {rc}")
+
     def get_prev_contact_counts(self) -> np.ndarray:
         out = np.zeros(self._num_envs, dtype=np.uint32)
         rc = self._lib.zeno_amd_world_get_prev_contact_counts(self._handle, out.ctypes.data_as(C.POINTER(C.c_uint32)))
