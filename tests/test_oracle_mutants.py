@@ -1,93 +1,219 @@
-"""Mutation check of the oracle pins: each plausible misreading of the contact solve, the
-lambda warm start and the accelerometer / gyro sensors, planted in a copy of the oracle's C
-source, must make tests/test_contact_solve.py fail.
+"""Mutation check of the oracle pins: each plausible misreading of the reference, planted in a
+copy of the oracle's C source, must make at least one of the oracle-pinning CPU test files
+fail. A misreading that survives marks a behaviour no pin covers, and the GPU kernel, which
+equals the oracle bit for bit, would share it unseen.
 
-Each mutant is compiled into a temporary directory and the pin tests run in a child pytest
-with ZENO_ORACLE_LIB pointing at it. The unmutated copy must pass the same run, so a failure
-is the mutation's doing.
+Every mutant is compiled into a temporary directory and the pin files run in a child pytest
+with ZENO_ORACLE_LIB pointing at it; the children run a few at a time. The unmutated copy
+must pass the same run, so a failure is the mutation's doing.
 """
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
 SRC = ROOT / "oracle" / "zeno_oracle.c"
-PINS = "tests/test_contact_solve.py"
+PINS = ["tests/test_oracle.py", "tests/test_model.py", "tests/test_hash.py", "tests/test_contact_solve.py",
+        "tests/test_oracle_pins.py", "tests/test_narrow_ext.py", "tests/test_ext_contacts.py"]
 
-# (name, original text, mutated text); the original must occur exactly once in the source.
+# (name, original text, mutated text, occurrences); the original must occur exactly that many
+# times in the source, and every occurrence is replaced. Leading whitespace picks one site
+# where the same line appears at two depths.
 MUTANTS = [
+    # contact solve (all_shaders.metal:1644-1793)
     ("friction sign of body a",
      "st3(Va, vsub(ld3(Va), vscale(impulse_t, inv_mass_a)));",
-     "st3(Va, vadd(ld3(Va), vscale(impulse_t, inv_mass_a)));"),
+     "st3(Va, vadd(ld3(Va), vscale(impulse_t, inv_mass_a)));", 1),
     ("friction sign of body b",
      "st3(Vb, vadd(ld3(Vb), vscale(impulse_t, inv_mass_b)));",
-     "st3(Vb, vsub(ld3(Vb), vscale(impulse_t, inv_mass_b)));"),
+     "st3(Vb, vsub(ld3(Vb), vscale(impulse_t, inv_mass_b)));", 1),
     ("friction cone clamp min -> max",
      "float j_t = fminf(j_t_desired, j_t_max);",
-     "float j_t = fmaxf(j_t_desired, j_t_max);"),
+     "float j_t = fmaxf(j_t_desired, j_t_max);", 1),
     ("friction cone without the stored impulse",
      "float j_n_acc = e->con[s].impulses[0] + j_n;",
-     "float j_n_acc = j_n;"),
+     "float j_n_acc = j_n;", 1),
     ("stored impulse is the running sum",
      "    e->con[s].impulses[0] = j_n;\n}",
-     "    e->con[s].impulses[0] = j_n_acc;\n}"),
+     "    e->con[s].impulses[0] = j_n_acc;\n}", 1),
     ("restitution threshold sign",
      "float vel_restitution = vel_normal < -0.5f ? restitution * vel_normal : 0.0f;",
-     "float vel_restitution = vel_normal > -0.5f ? restitution * vel_normal : 0.0f;"),
+     "float vel_restitution = vel_normal > -0.5f ? restitution * vel_normal : 0.0f;", 1),
     ("restitution dropped",
      "float j_n = (-(vel_normal + vel_restitution) + bias) / w_normal;",
-     "float j_n = (-(vel_normal) + bias) / w_normal;"),
+     "float j_n = (-(vel_normal) + bias) / w_normal;", 1),
+    # warm start and sensors (:1408-1444, 1838-1858)
     ("warm start factor 0.8 -> 0.5",
      "e->cs[i].state[0] = 0.8f * e->cs[i].state[1];",
-     "e->cs[i].state[0] = 0.5f * e->cs[i].state[1];"),
+     "e->cs[i].state[0] = 0.5f * e->cs[i].state[1];", 1),
     ("accelerometer rotates by q instead of its conjugate",
      "v3 lg = qrot(V(m->gravity[0], m->gravity[1], m->gravity[2]), qconj(q));",
-     "v3 lg = qrot(V(m->gravity[0], m->gravity[1], m->gravity[2]), q);"),
+     "v3 lg = qrot(V(m->gravity[0], m->gravity[1], m->gravity[2]), q);", 1),
     ("gyro reads the linear velocity",
      "case 3: case 10: { const float* w = P4(e->angvel, obj);",
-     "case 3: case 10: { const float* w = P4(e->vel, obj);"),
+     "case 3: case 10: { const float* w = P4(e->vel, obj);", 1),
+    ("frame position sensor reads the velocity",
+     "case 7: { const float* p = P4(e->pos, obj);",
+     "case 7: { const float* p = P4(e->vel, obj);", 1),
+    ("frame linear-velocity sensor reads the position",
+     "case 9: { const float* v = P4(e->vel, obj);",
+     "case 9: { const float* v = P4(e->pos, obj);", 1),
+    # compute_forces (:345-388)
+    ("gravity torque: cross product order swapped",
+     "v3 t = vcross(com_world, force);",
+     "v3 t = vcross(force, com_world);", 1),
+    ("gravity torque: COM offset not rotated",
+     "v3 com_world = qrot(ld3(e->m->bodies[b].com_offset), ld4(P4(e->quat, b)));",
+     "v3 com_world = ld3(e->m->bodies[b].com_offset);", 1),
+    # apply_joint_forces (:122-190)
+    ("joint force: parent reaction sign flipped",
+     "if (a > 0) add3(P4(dst, a), vneg(w));",
+     "if (a > 0) add3(P4(dst, a), w);", 1),
+    ("joint force: axis rotated by the child",
+     "v3 axis_world = qrot(ld3(jt->axis), ld4(P4(e->quat, a)));",
+     "v3 axis_world = qrot(ld3(jt->axis), ld4(P4(e->quat, b)));", 1),
+    ("joint force: threshold 1e-6 -> 0.1",
+     "if (fabsf(f) < 1e-6f) continue;",
+     "if (fabsf(f) < 0.1f) continue;", 1),
+    # integrate (:394-462)
+    ("integrate: linear damping dropped",
+     "vel = vscale(vel, 0.999f);", "vel = vel;", 1),
+    ("integrate: angular damping dropped",
+     "omega = vscale(omega, 0.999f);", "omega = omega;", 1),
+    ("integrate: body-frame angular velocity",
+     "q4 dq = qmul(Q(h.x, h.y, h.z, 0), quat);",
+     "q4 dq = qmul(quat, Q(h.x, h.y, h.z, 0));", 1),
+    # broad phase (:468-533) and its hash form (:556-703)
+    ("broad phase: margin 0.1 -> 0.2 (both sites)",
+     "float min_dist = radius_a + radius_b + 0.1f;",
+     "float min_dist = radius_a + radius_b + 0.2f;", 2),
+    ("broad phase: margin 0.1 -> 0.2 (hash site only)",
+     "                    float min_dist = radius_a + radius_b + 0.1f;",
+     "                    float min_dist = radius_a + radius_b + 0.2f;", 1),
+    ("broad phase: contype/conaffinity 'or' -> 'and' (both sites)",
+     "if ((group_a & mask_b) == 0 && (group_b & mask_a) == 0) continue;",
+     "if ((group_a & mask_b) == 0 || (group_b & mask_a) == 0) continue;", 2),
+    ("broad phase: same-body pairs kept (both sites)",
+     "if (body_a == body_b) continue;", "if (0) continue;", 2),
+    # narrow phase (:751-894)
+    ("capsule-plane: shallower endpoint chosen",
+     "                v3 deepest = d1 < d2 ? p1 : p2;",
+     "                v3 deepest = d1 < d2 ? p2 : p1;", 1),
+    ("sphere-sphere: contact point ra + pen/2",
+     "contact_point = vadd(pos_a, vscale(normal, ra - penetration * 0.5f));",
+     "contact_point = vadd(pos_a, vscale(normal, ra + penetration * 0.5f));", 1),
+    ("sphere-sphere: normal from b to a",
+     "normal = vdivs(diff, dist);", "normal = vneg(vdivs(diff, dist));", 1),
+    ("sphere-plane: plane position ignored",
+     "float signed_dist = vdot(vsub(sphere_pos, plane_pos), plane_normal);",
+     "float signed_dist = vdot(sphere_pos, plane_normal);", 1),
+    ("friction: arithmetic mean instead of geometric",
+     "float mu = sqrtf(ga->params[2] * gb->params[2]);",
+     "float mu = 0.5f * (ga->params[2] + gb->params[2]);", 1),
+    # solve_joints (:909-1399)
+    ("point constraint: parent COM lever dropped",
+     "v3 rc_a = vsub(r_a, qrot(ld3(e->m->bodies[ia].com_offset), quat_a));",
+     "v3 rc_a = r_a;", 1),
+    ("point constraint: child COM lever dropped",
+     "v3 rc_b = vsub(r_b, qrot(ld3(e->m->bodies[ib].com_offset), quat_b));",
+     "v3 rc_b = r_b;", 1),
+    ("slider: relative-quaternion target not conjugated",
+     "        q4 target = Q(c.limits[0], c.limits[1], c.limits[2], c.limits[3]);\n"
+     "        q4 qa = ld4(Qa), qb = ld4(Qb);\n"
+     "        q4 q_rel = qmul(qconj(qa), qb);\n"
+     "        q4 q_err = qmul(q_rel, qconj(target));",
+     "        q4 target = Q(c.limits[0], c.limits[1], c.limits[2], c.limits[3]);\n"
+     "        q4 qa = ld4(Qa), qb = ld4(Qb);\n"
+     "        q4 q_rel = qmul(qconj(qa), qb);\n"
+     "        q4 q_err = qmul(q_rel, target);", 1),
+    ("weld: relative-quaternion target not conjugated",
+     "        q4 target = ld4(c.axis_target);\n"
+     "        q4 qa = ld4(Qa), qb = ld4(Qb);\n"
+     "        q4 q_rel = qmul(qconj(qa), qb);\n"
+     "        q4 q_err = qmul(q_rel, qconj(target));",
+     "        q4 target = ld4(c.axis_target);\n"
+     "        q4 qa = ld4(Qa), qb = ld4(Qb);\n"
+     "        q4 q_rel = qmul(qconj(qa), qb);\n"
+     "        q4 q_err = qmul(q_rel, target);", 1),
+    # xpbd_update_velocities (:1922-1961)
+    ("velocity update: hemisphere flip dropped",
+     "if (dq.w < 0) dq = qneg(dq);", "(void)0;", 1),
+    # update_joint_states (:1550-1638)
+    ("hinge angle: world axis instead of the local one",
+     "            float sin_half = vdot(qxyz(q_rel), axis_local);\n"
+     "            e->jpos[j] = 2.0f * zo_atan2f(sin_half, q_rel.w);",
+     "            float sin_half = vdot(qxyz(q_rel), axis_world_a);\n"
+     "            e->jpos[j] = 2.0f * zo_atan2f(sin_half, q_rel.w);", 1),
+    ("hinge angle: relative rotation q_b conj(q_a)",
+     "q4 q_rel = qmul(qconj(q_a), q_b);", "q4 q_rel = qmul(q_b, qconj(q_a));", 1),
+    ("hinge rate: local axis instead of the parent-frame one",
+     "e->jvel[j] = vdot(vsub(w_b, w_a), axis_world_a);",
+     "e->jvel[j] = vdot(vsub(w_b, w_a), axis_local);", 1),
+    ("slide state: child anchor dropped from the position",
+     "v3 diff = vsub(vadd(p_b, r_b), vadd(p_a, r_a));",
+     "v3 diff = vsub(p_b, vadd(p_a, r_a));", 1),
+    ("slide state: child lever dropped from the velocity",
+     "v3 v_pt_b = vadd(v_b, vcross(w_b, r_b));", "v3 v_pt_b = v_b;", 1),
+    ("slide state: parent lever dropped from the velocity",
+     "v3 v_pt_a = vadd(v_a, vcross(w_a, r_a));", "v3 v_pt_a = v_a;", 1),
+    # World.step (world.zig:736-746)
+    ("accelerations divided by the substep dt",
+     "float inv_step = m->timestep > 0 ? 1.0f / m->timestep : 0.0f;",
+     "float inv_step = dt > 0 ? 1.0f / dt : 0.0f;", 1),
 ]
 
 
 def _build(src_text: str, out: Path) -> None:
-    gcc = shutil.which("gcc")
     c = out.with_suffix(".c")
     c.write_text(src_text)
     shutil.copy(ROOT / "oracle" / "zeno_oracle.h", out.parent / "zeno_oracle.h")
-    r = subprocess.run([gcc, "-O1", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
-                        str(c), "-o", str(out), "-lm"], capture_output=True, text=True)
+    r = subprocess.run([shutil.which("gcc"), "-O1", "-std=c11", "-fPIC", "-shared", "-ffp-contract=off",
+                        "-fno-fast-math", str(c), "-o", str(out), "-lm"], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
 
 
 def _run_pins(lib: Path) -> subprocess.CompletedProcess:
-    env = dict(os.environ, ZENO_ORACLE_LIB=str(lib), PYTHONPATH=str(ROOT))
-    return subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", PINS],
-                          cwd=str(ROOT), env=env, capture_output=True, text=True, timeout=300)
+    env = dict(os.environ, ZENO_ORACLE_LIB=str(lib), PYTHONPATH=str(ROOT), OMP_NUM_THREADS="1")
+    return subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", *PINS],
+                          cwd=str(ROOT), env=env, capture_output=True, text=True, timeout=600)
+
+
+def _build_and_run(src_text: str, workdir: Path) -> subprocess.CompletedProcess:
+    workdir.mkdir(parents=True, exist_ok=True)
+    lib = workdir / "oracle.so"
+    _build(src_text, lib)
+    return _run_pins(lib)
 
 
 @pytest.fixture(scope="module")
-def source():
+def results():
+    """Runs the unmutated copy and every mutant (4 child processes at a time)."""
     if shutil.which("gcc") is None:
         pytest.skip("gcc is required")
-    return SRC.read_text()
+    source = SRC.read_text()
+    jobs = {"<unmutated>": source}
+    for name, orig, mut, n in MUTANTS:
+        assert source.count(orig) == n, f"mutation site for '{name}' found {source.count(orig)} times, not {n}"
+        jobs[name] = source.replace(orig, mut)
+    with tempfile.TemporaryDirectory() as tmp:
+        with ThreadPoolExecutor(max_workers=4) as pool:
+            futs = {k: pool.submit(_build_and_run, v, Path(tmp) / f"m{i}") for i, (k, v) in enumerate(jobs.items())}
+            yield {k: f.result() for k, f in futs.items()}
 
 
-def test_unmutated_copy_passes(source, tmp_path):
-    lib = tmp_path / "oracle_ref.so"
-    _build(source, lib)
-    r = _run_pins(lib)
+def test_unmutated_copy_passes(results):
+    r = results["<unmutated>"]
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
 
 
-@pytest.mark.parametrize("name,orig,mut", MUTANTS, ids=[m[0] for m in MUTANTS])
-def test_mutant_is_caught(source, tmp_path, name, orig, mut):
-    assert source.count(orig) == 1, f"mutation site for '{name}' not found exactly once"
-    lib = tmp_path / "oracle_mut.so"
-    _build(source.replace(orig, mut), lib)
-    r = _run_pins(lib)
+@pytest.mark.parametrize("name", [m[0] for m in MUTANTS])
+def test_mutant_is_caught(results, name):
+    r = results[name]
     assert r.returncode != 0, f"mutant '{name}' passed every pin test"
     assert "failed" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]

@@ -1,0 +1,520 @@
+"""Pins the oracle (oracle/zeno_oracle.c) where its earlier checks left it open: closed forms,
+physical laws and definitions computed here in float64, none of them a restatement of the
+oracle's code. Each case is built so that a plausible misreading of the reference changes
+its answer; tests/test_oracle_mutants.py plants those misreadings and checks that they fail.
+
+  compute_forces         gravity torque about the body origin (r_com x m g) with the COM
+                         offset rotated into the world frame (all_shaders.metal:383-387)
+  apply_joint_forces     a motor between two dynamic bodies: equal and opposite torques
+                         about the PARENT's axis, nothing below |tau| 1e-6 (:141-189)
+  narrow_phase           capsule-plane: the deeper endpoint, both tilts (:862-880);
+                         sphere-sphere: the midpoint of the overlap segment (:806);
+                         friction: geometric mean of the two geoms' mu (:885)
+  broad_phase            the 0.1 proxy margin from both sides, and MuJoCo's contype /
+                         conaffinity rule on asymmetric masks (:490-519)
+  velocity update        a rotation of more than pi within one substep is reported as the
+                         shortest arc (:1957)
+  update_joint_states    slide: displacement and relative speed of the two anchor points
+                         along the parent's axis; hinge: rotation about the LOCAL axis (Q27)
+                         (:1591-1636)
+  read_sensors           frame position / quaternion / linear and angular velocity sensors
+                         pointed at a moving body (:1857-1880)
+  World.step             accelerations at substeps = 2 divide by the whole step's timestep
+                         (world.zig:736-746)
+  solve_joints           point constraint on offset-COM bodies: the correction turns each
+                         body about its COM (:1010-1030); slider and weld hold their
+                         build-time relative orientation (:1348-1391, world.zig:397-415)
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zeno_amd.model import load_model
+
+G = 9.81
+
+
+def _qaxis(axis, theta):
+    a = np.asarray(axis, np.float64)
+    a = a / np.linalg.norm(a)
+    return np.array([*(np.sin(theta / 2) * a), np.cos(theta / 2)])
+
+
+def _qmul(a, b):
+    ax, ay, az, aw = a
+    bx, by, bz, bw = b
+    return np.array([aw * bx + ax * bw + ay * bz - az * by,
+                     aw * by - ax * bz + ay * bw + az * bx,
+                     aw * bz + ax * by - ay * bx + az * bw,
+                     aw * bw - ax * bx - ay * by - az * bz])
+
+
+def _qconj(q):
+    return np.array([-q[0], -q[1], -q[2], q[3]])
+
+
+def _rotmat(q):
+    x, y, z, w = np.asarray(q, np.float64) / np.linalg.norm(q)
+    return np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - z * w), 2 * (x * z + y * w)],
+                     [2 * (x * y + z * w), 1 - 2 * (x * x + z * z), 2 * (y * z - x * w)],
+                     [2 * (x * z - y * w), 2 * (y * z + x * w), 1 - 2 * (x * x + y * y)]])
+
+
+def _world(xml, num_envs=1, gravity=None, iterations=4, **kw):
+    m = load_model(mjcf_string=xml)
+    w = O.OracleWorld(m, num_envs, contact_iterations=iterations, **kw)
+    if gravity is not None:
+        w.gravity = list(gravity)
+    return m, w
+
+
+def _set(w, b, pos=None, quat=None, vel=None, angvel=None):
+    p, q = w.positions.copy(), w.quaternions.copy()
+    v, av = w.velocities.copy(), w.angular_velocities.copy()
+    for arr, val in ((p, pos), (v, vel), (av, angvel)):
+        if val is not None:
+            arr[0, b, :3] = val
+    if quat is not None:
+        q[0, b] = np.asarray(quat, np.float32)
+    w.reset_to_state(p, q, v, av)
+
+
+# ---------------------------------------------------------------- compute_forces
+
+OFFSET_COM_FREE = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="b" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1" pos="0.2 0 0" mass="2"/></body>
+</worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("turn", [0.0, np.pi / 2, 1.1])
+def test_gravity_torque_about_the_body_origin(turn):
+    """Gravity acts at the COM; about the body origin it exerts tau = (R c) x (m g), with c the
+    COM offset in the body frame (0.2, 0, 0) and R the body's rotation. A quarter turn about z
+    moves the lever to +y, so tau = (0.2, 0, 0)-turned x (0, 0, -2 g) = (-0.4 g, 0, 0)."""
+    m, w = _world(OFFSET_COM_FREE)
+    np.testing.assert_array_equal(m["bodies"]["com_offset"][1, :3], np.float32([0.2, 0, 0]))
+    q = _qaxis([0, 0, 1], turn)
+    _set(w, 1, quat=q)
+    w.step(None)
+    lever = _rotmat(np.float32(q)) @ [0.2, 0.0, 0.0]
+    want = np.cross(lever, [0.0, 0.0, -2.0 * G])
+    np.testing.assert_allclose(w.torques[0, 1, :3], want, atol=2e-6)
+    np.testing.assert_allclose(w.forces[0, 1, :3], [0, 0, -2.0 * G], rtol=1e-6)
+    if turn == np.pi / 2:
+        np.testing.assert_allclose(w.torques[0, 1, :3], [-0.4 * G, 0, 0], atol=2e-6)
+
+
+# ---------------------------------------------------------------- apply_joint_forces
+
+MOTOR_PAIR = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 2"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/>
+<body name="b" pos="0 0 -0.5"><joint name="h" type="{kind}" axis="0 1 0"/><geom type="sphere" size="0.1" mass="1"/></body>
+</body></worldbody>
+<actuator><motor joint="h" gear="1" ctrlrange="-1 1"/></actuator></mujoco>"""
+
+
+@pytest.mark.parametrize("kind,dst", [("hinge", "torques"), ("slide", "forces")])
+@pytest.mark.parametrize("ctrl", [0.5, -0.05, 2e-6])
+def test_motor_between_dynamic_bodies(kind, dst, ctrl):
+    """The joint's generalised force f acts on the child along the joint axis expressed in
+    the PARENT's frame and on the parent with the opposite sign (Newton's third law), so the
+    pair's sum is zero. Parent and child are given different orientations, so the parent's
+    frame is told apart from the child's. A hinge takes a torque, a slide a force. Without
+    gravity and with both COMs at the body origins nothing else enters either sum."""
+    _, w = _world(MOTOR_PAIR.format(kind=kind), gravity=(0, 0, 0))
+    qa = _qaxis([1, 0, 0], np.pi / 2)    # parent's y axis -> world z
+    qb = _qaxis([0, 0, 1], np.pi / 2)    # child's y axis -> world -x
+    _set(w, 1, quat=qa)
+    _set(w, 2, quat=qb)
+    w.step(np.array([[ctrl]], np.float32))
+    axis = _rotmat(np.float32(qa)) @ [0.0, 1.0, 0.0]
+    got = getattr(w, dst)
+    tol = 1e-6 * abs(ctrl)
+    np.testing.assert_allclose(got[0, 2, :3], ctrl * axis, rtol=1e-5, atol=tol)
+    np.testing.assert_allclose(got[0, 1, :3], -ctrl * axis, rtol=1e-5, atol=tol)
+    np.testing.assert_allclose(got[0, 1, :3] + got[0, 2, :3], 0.0, atol=1e-12)
+
+
+@pytest.mark.parametrize("ctrl", [9e-7, -5e-7, 0.0])
+def test_motor_below_threshold_applies_nothing(ctrl):
+    """Generalised forces with |f| < 1e-6 are dropped (Q14)."""
+    _, w = _world(MOTOR_PAIR.format(kind="hinge"), gravity=(0, 0, 0))
+    w.step(np.array([[ctrl]], np.float32))
+    assert np.all(w.torques[0] == 0)
+
+
+# ---------------------------------------------------------------- narrow phase
+
+TILTED_CAPSULE = """<mujoco><worldbody><geom type="plane" size="5 5 0.1"/>
+<body name="c" pos="0.5 -0.3 {h}"><joint type="free"/><geom type="capsule" size="0.05 0.3" quat="{q}" mass="1"/></body>
+</worldbody></mujoco>"""
+
+
+def tilted_capsule_mjcf(tilt, h):
+    q = _qaxis([0, 1, 0], tilt)
+    return TILTED_CAPSULE.format(h=h, q=" ".join(f"{v:.8f}" for v in (q[3], q[0], q[1], q[2])))
+
+
+@pytest.mark.parametrize("tilt,h", [(0.6, 0.28), (-0.6, 0.28), (1.4, 0.1), (-1.4, 0.1), (2.6, 0.28)])
+def test_capsule_plane_contact_at_the_deeper_endpoint(tilt, h):
+    """A capsule (radius 0.05, half length 0.3) whose axis is tilted by `tilt` about y (the
+    geom's own quaternion sets the axis, Q3) touches the plane z = 0 at its lower endpoint:
+    contact x, y are that endpoint's, z is 0, and the depth is r - z_end. With |tilt| = 1.4
+    both endpoints are below r and the deeper one counts."""
+    m = load_model(mjcf_string=tilted_capsule_mjcf(tilt, h))
+    np.testing.assert_allclose(m["geoms"]["quat"][1], _qaxis([0, 1, 0], tilt), atol=1e-7)
+    w = O.OracleWorld(m, 1)
+    O.collide_env(w, 0)
+    axis = _rotmat(m["geoms"]["quat"][1]) @ [0.0, 0.0, 1.0]
+    centre = np.array([0.5, -0.3, h])
+    ends = [centre - 0.3 * axis, centre + 0.3 * axis]
+    low = min(ends, key=lambda e: e[2])
+    c = w.contacts[0][0]
+    assert list(c["indices"][:2]) == [0, 1]
+    np.testing.assert_allclose(c["position_pen"][:3], [low[0], low[1], 0.0], atol=2e-6)
+    np.testing.assert_allclose(c["position_pen"][3], 0.05 - low[2], atol=2e-6)
+    np.testing.assert_array_equal(c["normal_friction"][:3], [0, 0, -1])
+
+
+SPHERES = """<mujoco><option gravity="0 0 0"/><worldbody>
+<body name="a" pos="{pa}"><joint type="free"/><geom type="sphere" size="{ra}" mass="1" {ga}/></body>
+<body name="b" pos="{pb}"><joint type="free"/><geom type="sphere" size="{rb}" mass="1" {gb}/></body>
+</worldbody></mujoco>"""
+
+
+def _spheres(pa, ra, pb, rb, ga="", gb=""):
+    fmt = lambda v: " ".join(f"{x:.6f}" for x in v)
+    m = load_model(mjcf_string=SPHERES.format(pa=fmt(pa), pb=fmt(pb), ra=ra, rb=rb, ga=ga, gb=gb))
+    w = O.OracleWorld(m, 1)
+    O.collide_env(w, 0)
+    return m, w
+
+
+def test_sphere_sphere_contact_point_is_the_overlap_midpoint():
+    """Unequal spheres (0.3 and 0.6) 0.8 apart along a diagonal overlap by 0.1 on the
+    segment from b's near surface to a's near surface; the contact point is its midpoint
+    and the normal points from a to b."""
+    d = np.array([2.0, -1.0, 2.0]) / 3.0
+    pa = np.array([0.3, 0.4, 5.0])
+    pb = pa + 0.8 * d
+    _, w = _spheres(pa, 0.3, pb, 0.6)
+    assert int(w.contact_counts[0]) == 1
+    c = w.contacts[0][0]
+    mid = 0.5 * ((pa + 0.3 * d) + (pb - 0.6 * d))
+    np.testing.assert_allclose(c["position_pen"][:3], mid, atol=2e-6)
+    np.testing.assert_allclose(c["position_pen"][3], 0.1, atol=2e-6)
+    np.testing.assert_allclose(c["normal_friction"][:3], d, atol=2e-6)
+
+
+@pytest.mark.parametrize("mua,mub", [(0.25, 1.0), (0.09, 1.0), (0.04, 0.25)])
+def test_friction_is_the_geometric_mean(mua, mub):
+    """The contact's mu combines the geoms' coefficients as sqrt(mu_a mu_b) (Q6); MJCF reads
+    the first of the three friction values."""
+    _, w = _spheres((0, 0, 5), 0.5, (0.8, 0, 5), 0.5, ga=f'friction="{mua} 0.005 0.0001"',
+                    gb=f'friction="{mub} 0.005 0.0001"')
+    np.testing.assert_allclose(w.contacts[0][0]["normal_friction"][3], np.sqrt(mua * mub), rtol=1e-6)
+
+
+# ---------------------------------------------------------------- broad phase
+
+@pytest.mark.parametrize("gap,listed", [(-0.001, True), (0.001, False), (-0.05, True), (0.05, False)])
+def test_broad_phase_margin(gap, listed):
+    """Two spheres (r 0.5) are a candidate pair while their centres are closer than
+    r_a + r_b + 0.1 = 1.1; the narrow phase then finds no contact (no overlap)."""
+    _, w = _spheres((0, 0, 5), 0.5, (1.1 + gap, 0, 5), 0.5)
+    assert int(w.contact_counts[0]) == (1 if listed else 0)
+    if listed:
+        assert w.contacts[0][0]["position_pen"][3] == -1.0
+
+
+@pytest.mark.parametrize("ta,aa,tb,ab", [(1, 0, 0, 1), (0, 1, 1, 0), (3, 0, 0, 2), (2, 2, 1, 1), (0, 0, 1, 1),
+                                         (4, 1, 2, 4), (1, 1, 1, 1)])
+def test_contype_conaffinity_rule(ta, aa, tb, ab):
+    """MuJoCo's filter: two geoms may collide when (contype_a & conaffinity_b) or
+    (contype_b & conaffinity_a) is non-zero."""
+    _, w = _spheres((0, 0, 5), 0.5, (0.5, 0, 5), 0.5, ga=f'contype="{ta}" conaffinity="{aa}"',
+                    gb=f'contype="{tb}" conaffinity="{ab}"')
+    want = (ta & ab) != 0 or (tb & aa) != 0
+    assert int(w.contact_counts[0]) == int(want)
+
+
+# ---------------------------------------------------------------- velocity update
+
+HINGE_LIMIT = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="b" pos="0 0 1"><joint name="h" type="hinge" axis="0 1 0" range="-0.5 0.5"/>
+<geom type="sphere" size="0.1" mass="1"/></body></worldbody>
+<sensor><jointpos joint="h"/><jointvel joint="h"/></sensor></mujoco>"""
+
+
+def test_velocity_update_reports_the_shortest_arc():
+    """The angular limit turns the child further from its limit each iteration (the
+    reference's sign; pinned in test_oracle.py): from 0.8 rad, four iterations add 3.63 rad
+    about y. That exceeds pi, and the rotation from the substep's start to its end is the
+    same as one of 3.63 - 2 pi; the velocity update reports that shorter arc,
+    omega_y = 2 sin(theta / 2) / dt with theta in (-pi, pi]."""
+    _, w = _world(HINGE_LIMIT, gravity=(0, 0, 0))
+    _set(w, 1, quat=_qaxis([0, 1, 0], 0.8))
+    w.step(None)
+    angle = 0.8
+    for _ in range(4):
+        angle += 2 * np.arctan(-(0.5 - angle) / 2)
+    turned = angle - 0.8
+    assert turned > np.pi
+    short = turned - 2 * np.pi
+    want = 2 * np.sin(short / 2) / 0.01
+    np.testing.assert_allclose(w.angular_velocities[0, 1, :3], [0, want, 0], rtol=1e-3, atol=1e-3)
+    np.testing.assert_allclose(w.joint_velocities[0, 0], want, rtol=1e-3)
+
+
+def test_velocity_update_small_rotation():
+    """A rotation below pi: omega = 2 sin(theta / 2) / dt about the same axis."""
+    _, w = _world(HINGE_LIMIT, gravity=(0, 0, 0), iterations=1)
+    _set(w, 1, quat=_qaxis([0, 1, 0], 0.8))
+    w.step(None)
+    turned = 2 * np.arctan(0.3 / 2)
+    np.testing.assert_allclose(w.angular_velocities[0, 1, 1], 2 * np.sin(turned / 2) / 0.01, rtol=1e-4)
+
+
+# ---------------------------------------------------------------- joint states
+
+SLIDE_PAIR = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 2"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/>
+<body name="b" pos="0.3 0 0.2"><joint name="s" type="slide" axis="1 0 0" pos="0.1 0.05 0"/>
+<geom type="sphere" size="0.1" mass="1"/></body></body></worldbody>
+<sensor><jointpos joint="s"/><jointvel joint="s"/></sensor></mujoco>"""
+
+
+def _anchor_state(m, w, j, a, b):
+    """Anchor points of joint j on bodies a and b and their velocities, in float64 from the
+    state after the step."""
+    jt = m["joints"][j]
+    p = w.positions[0].astype(np.float64)
+    q = w.quaternions[0].astype(np.float64)
+    v = w.velocities[0].astype(np.float64)
+    om = w.angular_velocities[0].astype(np.float64)
+    ra = _rotmat(q[a]) @ jt["anchor_parent"][:3].astype(np.float64)
+    rb = _rotmat(q[b]) @ jt["anchor_child"][:3].astype(np.float64)
+    axis = _rotmat(q[a]) @ jt["axis"][:3].astype(np.float64)
+    pa, pb = p[a, :3] + ra, p[b, :3] + rb
+    va = v[a, :3] + np.cross(om[a, :3], ra)
+    vb = v[b, :3] + np.cross(om[b, :3], rb)
+    return pa, pb, va, vb, axis
+
+
+@pytest.mark.parametrize("iterations", [0, 4])
+def test_slide_joint_state_is_anchor_displacement(iterations):
+    """A slide joint's coordinate is the child anchor's displacement from the parent anchor
+    along the parent's axis, and its rate the relative velocity of those two points along
+    that axis. The anchors sit off both bodies' centres (parent anchor = child pos + joint
+    pos; child anchor = joint pos, Q19) and both bodies turn and spin, so the lever terms
+    matter. With zero iterations the solver is off and the bodies move freely."""
+    m, w = _world(SLIDE_PAIR, gravity=(0, 0, 0), iterations=iterations)
+    np.testing.assert_allclose(m["joints"]["anchor_child"][1, :3], [0.1, 0.05, 0])
+    _set(w, 1, quat=_qaxis([0, 0, 1], 0.3), vel=(0.2, -0.1, 0.05), angvel=(0.5, 0.0, 0.0))
+    _set(w, 2, pos=(0.35, 0.1, 2.25), quat=_qaxis([1, 2, 3], 0.7), vel=(-0.3, 0.4, 0.1), angvel=(0.3, -0.2, 2.0))
+    w.step(None)
+    pa, pb, va, vb, axis = _anchor_state(m, w, 1, 1, 2)
+    np.testing.assert_allclose(w.joint_positions[0, 1], np.dot(pb - pa, axis), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(w.joint_velocities[0, 1], np.dot(vb - va, axis), rtol=1e-4, atol=1e-5)
+    np.testing.assert_array_equal(w.observations[0, :2], [w.joint_positions[0, 1], w.joint_velocities[0, 1]])
+
+
+HINGE_PAIR = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 2"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/>
+<body name="b" pos="0 0 -0.5"><joint name="h" type="hinge" axis="0 1 0"/>
+<geom type="sphere" size="0.1" mass="1"/></body></body></worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("theta", [0.4, -1.2, 2.5])
+def test_hinge_angle_is_about_the_local_axis(theta):
+    """The hinge coordinate is the child's rotation relative to the parent about the joint
+    axis in the PARENT's frame: with the parent turned a quarter about x and the child at
+    q_a * rot(y, theta), the joint reads theta; its rate is (omega_b - omega_a) along the
+    parent-frame axis (Q27). Solver off, no velocities: the state stays put."""
+    _, w = _world(HINGE_PAIR, gravity=(0, 0, 0), iterations=0)
+    qa = _qaxis([1, 0, 0], np.pi / 2)
+    qb = _qmul(qa, _qaxis([0, 1, 0], theta))
+    _set(w, 1, quat=qa)
+    _set(w, 2, pos=(0, 0.5, 2), quat=qb)
+    w.step(None)
+    np.testing.assert_allclose(w.joint_positions[0, 1], theta, atol=2e-6)
+
+
+def test_hinge_rate_along_the_parent_axis():
+    _, w = _world(HINGE_PAIR, gravity=(0, 0, 0), iterations=0)
+    qa = _qaxis([1, 0, 0], np.pi / 2)
+    _set(w, 1, quat=qa, angvel=(0.1, 0.2, -0.3))
+    _set(w, 2, pos=(0, 0.5, 2), quat=_qmul(qa, _qaxis([0, 1, 0], 0.3)), angvel=(0.4, -0.5, 1.5))
+    w.step(None)
+    q = w.quaternions[0].astype(np.float64)
+    axis = _rotmat(q[1]) @ [0.0, 1.0, 0.0]
+    rel = w.angular_velocities[0, 2, :3].astype(np.float64) - w.angular_velocities[0, 1, :3]
+    np.testing.assert_allclose(w.joint_velocities[0, 1], np.dot(rel, axis), rtol=1e-5, atol=1e-6)
+    q_rel = _qmul(_qconj(q[1]), q[2])
+    np.testing.assert_allclose(w.joint_positions[0, 1], 2 * np.arctan2(q_rel[1], q_rel[3]), atol=2e-6)
+
+
+# ---------------------------------------------------------------- sensors
+
+FRAME_SENSORS = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="b" pos="0.2 -0.1 1"><joint type="free"/><geom type="sphere" size="0.1" mass="2"/></body></worldbody>
+<sensor><framepos objtype="body" objname="b"/><framequat objtype="body" objname="b"/>
+<framelinvel objtype="body" objname="b"/><frameangvel objtype="body" objname="b"/></sensor></mujoco>"""
+
+
+def test_frame_sensors_track_a_moving_body():
+    """Frame sensors report their object's position, orientation, linear and angular
+    velocity. The parser leaves the object at body 0 (Q19), so the records are pointed at the
+    falling, spinning body here; obs is 3 + 4 + 3 + 3 values in sensor order."""
+    m, w = _world(FRAME_SENSORS)
+    assert list(m["sensors"]["type_object"][:, 0]) == [7, 8, 9, 10]
+    m["sensors"]["type_object"][:, 1] = 1
+    w = O.OracleWorld(m, 1)
+    _set(w, 1, vel=(1.0, 0.5, 2.0), angvel=(0.3, -0.4, 1.0))
+    for _ in range(3):
+        w.step(None)
+    o = w.observations[0]
+    np.testing.assert_array_equal(o[0:3], w.positions[0, 1, :3])
+    np.testing.assert_array_equal(o[3:7], w.quaternions[0, 1])
+    np.testing.assert_array_equal(o[7:10], w.velocities[0, 1, :3])
+    np.testing.assert_array_equal(o[10:13], w.angular_velocities[0, 1, :3])
+    assert np.all(np.abs(o[7:10] - o[0:3]) > 0.1)  # the body is away from its own velocity
+
+
+# ---------------------------------------------------------------- World.step accelerations
+
+FREE_BALL = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="ball" pos="0 0 0"><joint type="free"/><geom type="sphere" size="0.1" mass="2"/></body>
+</worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("substeps", [1, 2, 4])
+def test_acceleration_over_the_whole_step(substeps):
+    """From rest, k substeps of h = dt / k give v_k = g h (0.999 + ... + 0.999^k) (semi-implicit
+    Euler with damping, the velocity update returns the same v); the reported acceleration is
+    the velocity change over the whole call divided by the call's timestep dt, not by h."""
+    _, w = _world(FREE_BALL)
+    w.step(None, substeps=substeps)
+    h = 0.01 / substeps
+    v = 0.0
+    for _ in range(substeps):
+        v = (v - G * h) * 0.999
+    np.testing.assert_allclose(w.velocities[0, 1, 2], v, rtol=1e-5)
+    np.testing.assert_allclose(w.accelerations[0, 1, 2], v / 0.01, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- solve_joints
+
+BALL_OFFSET_COM = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1" pos="0 0.2 0" mass="1"/>
+<body name="b" pos="1 0 0"><joint type="ball"/><geom type="sphere" size="0.1" pos="0 0 0.1" mass="3"/></body>
+</body></worldbody></mujoco>"""
+
+
+def test_point_constraint_turns_each_body_about_its_com():
+    """Ball joint between two free bodies whose COMs sit off their origins (parent (0, 0.2, 0),
+    child (0, 0, 0.1)); the child is pulled 0.3 along x off the anchor. One iteration moves
+    both bodies along x by the inverse-mass split (the anchor levers are parallel to the
+    gap, so they add no effective mass) and gives each the angular kick of its impulse
+    applied at the anchor about its COM: I^-1 ((anchor - com) x dp)."""
+    m, w = _world(BALL_OFFSET_COM, gravity=(0, 0, 0), iterations=1)
+    np.testing.assert_allclose(m["bodies"]["com_offset"][1:3, :3], [[0, 0.2, 0], [0, 0, 0.1]], atol=1e-7)
+    _set(w, 2, pos=(1.3, 0, 1))
+    w.step(None)
+    imi = m["inv_mass_inertia"].astype(np.float64)
+    wsum = imi[1, 0] + imi[2, 0]
+    J = 0.3 / wsum                                 # |dp| of the correction
+    dp_a, dp_b = np.array([J, 0, 0]), np.array([-J, 0, 0])
+    np.testing.assert_allclose(w.positions[0, 1, :3], [J * imi[1, 0], 0, 1], atol=1e-6)
+    np.testing.assert_allclose(w.positions[0, 2, :3], [1.3 - J * imi[2, 0], 0, 1], atol=1e-6)
+    for b, anchor, com, dp in ((1, [1.0, 0, 0], [0, 0.2, 0], dp_a), (2, [0, 0, 0], [0, 0, 0.1], dp_b)):
+        kick = imi[b, 1:] * np.cross(np.subtract(anchor, com), dp)
+        ang = np.linalg.norm(kick)
+        want = _qaxis(kick, 2 * np.arctan(ang / 2))
+        np.testing.assert_allclose(w.quaternions[0, b], want, atol=2e-6)
+
+
+ROTATED_CHILD = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="c" pos="0 0 1" quat="{q}">{joint}<geom type="sphere" size="0.1" mass="1"/></body>
+</worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("joint", ['<joint type="slide" axis="1 0 0"/>', ""])
+def test_slider_and_weld_hold_the_build_time_orientation(joint):
+    """A slider (slide joint) or weld (no joint) stores the child's orientation relative to
+    its parent at build time (world.zig:397-415; the child here is turned 90 degrees about
+    z against the world body). At that pose nothing moves; turned a further 0.3 rad about x,
+    one iteration rotates it back by 2 atan(0.15) toward the stored pose."""
+    qc = _qaxis([0, 0, 1], np.pi / 2)
+    xml = ROTATED_CHILD.format(q=" ".join(f"{v:.7f}" for v in (qc[3], qc[0], qc[1], qc[2])), joint=joint)
+    m, w = _world(xml, gravity=(0, 0, 0), iterations=1)
+    np.testing.assert_allclose(m["init_quaternions"][1], qc, atol=1e-7)
+    q0 = w.quaternions.copy()
+    w.step(None)
+    np.testing.assert_allclose(w.quaternions, q0, atol=1e-7)
+    _, w = _world(xml, gravity=(0, 0, 0), iterations=1)
+    _set(w, 1, quat=_qmul(_qaxis([1, 0, 0], 0.3), qc))
+    w.step(None)
+    q = w.quaternions[0, 1].astype(np.float64)
+    err = _qmul(q, _qconj(qc))
+    err = err if err[3] >= 0 else -err
+    np.testing.assert_allclose(err, _qaxis([1, 0, 0], 0.3 - 2 * np.arctan(0.15)), atol=2e-6)
+
+
+# ---------------------------------------------------------------- integrate, plane height, same body
+
+SPINNER = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="b" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/></body>
+</worldbody></mujoco>"""
+
+
+def test_integrate_turns_about_the_world_frame_angular_velocity():
+    """omega is a world-frame vector: a body turned a quarter about x and spinning about
+    world z ends the step at rot(z, phi) * q0 with phi = 2 atan(|omega'| dt / 2),
+    omega' = 0.999 omega (damping); a body-frame reading would give q0 * rot(z, phi)."""
+    _, w = _world(SPINNER, gravity=(0, 0, 0))
+    q0 = _qaxis([1, 0, 0], np.pi / 2)
+    _set(w, 1, quat=q0, angvel=(0, 0, 3.0))
+    w.step(None)
+    phi = 2 * np.arctan(0.999 * 3.0 * 0.01 / 2)
+    np.testing.assert_allclose(w.quaternions[0, 1], _qmul(_qaxis([0, 0, 1], phi), q0), atol=2e-6)
+
+
+RAISED_PLANE = """<mujoco><worldbody><geom type="plane" pos="0 0 0.5" size="5 5 0.1"/>
+<body name="s" pos="0 0 0.55"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/></body>
+<body name="c" pos="2 0 0.3"><joint type="free"/><geom type="capsule" size="0.05 0.2" mass="1"/></body>
+</worldbody></mujoco>"""
+
+
+def test_plane_height_sphere_uses_it_capsule_does_not():
+    """Sphere-plane measures the sphere's height above the plane geom's position (the plane
+    at z = 0.5: depth 0.1 - 0.05 = 0.05, contact point midway into the overlap); capsule-plane
+    takes the plane at z = 0 whatever its position (Q3): the vertical capsule's lower end
+    at 0.1 is clear of it."""
+    m = load_model(mjcf_string=RAISED_PLANE)
+    w = O.OracleWorld(m, 1)
+    O.collide_env(w, 0)
+    n = int(w.contact_counts[0])
+    idx = w.contacts[0]["indices"][:n]
+    sp = [i for i in range(n) if set(idx[i, 2:]) == {0, 1}]
+    cp = [i for i in range(n) if set(idx[i, 2:]) == {0, 2}]
+    c = w.contacts[0][sp[0]]
+    np.testing.assert_allclose(c["position_pen"], [0, 0, 0.475, 0.05], atol=2e-6)
+    assert w.contacts[0][cp[0]]["position_pen"][3] == -1.0
+
+
+TWO_GEOMS_ONE_BODY = """<mujoco><worldbody>
+<body name="b" pos="0 0 5"><joint type="free"/><geom type="sphere" size="0.3" mass="1"/>
+<geom type="sphere" size="0.3" pos="0.2 0 0" mass="1"/></body>
+<body name="o" pos="0.5 0 5"><joint type="free"/><geom type="sphere" size="0.3" mass="1"/></body>
+</worldbody></mujoco>"""
+
+
+def test_geoms_of_one_body_never_pair():
+    """Overlapping geoms of the same body are not candidates; each pairs with the other
+    body's geom, in (g, g') order."""
+    m = load_model(mjcf_string=TWO_GEOMS_ONE_BODY)
+    w = O.OracleWorld(m, 1)
+    O.collide_env(w, 0)
+    assert int(w.contact_counts[0]) == 2
+    np.testing.assert_array_equal(w.contacts[0]["indices"][:2], [[1, 2, 0, 2], [1, 2, 1, 2]])
