@@ -55,7 +55,8 @@ def test_vector_env_reset_step_and_autoreset():
     assert truncated.all() and info["final_observation"][0] is not None
     # The next step first resets every env (auto-reset), then steps once.
     env.step(np.zeros((8, 1), np.float32))
-    assert np.all(info["_elapsed_steps"] == 4) and np.all(env._elapsed_steps == 1)
+    assert np.all(info["_elapsed_steps"] == 4) and np.all(env.elapsed_steps == 1)
+    assert info["_final_observation"].all() and info["final_info"][3] == {"episode_step": 4}
     assert check_env(env) is True
     env.step_async(np.zeros((8, 1), np.float32))
     assert len(env.step_wait()) == 5

@@ -56,8 +56,19 @@ class ZenoEnv:
         self.world = ZenoWorld(mjcf_path=mjcf_path, mjcf_string=mjcf_string, num_envs=num_envs,
                                timestep=timestep, contact_iterations=contact_iterations,
                                max_contacts_per_env=max_contacts_per_env, seed=seed, substeps=substeps)
+        self.mjcf_path = mjcf_path
         self.max_episode_steps = EPISODE_LIMIT
         self.steps_since_reset = 0
+
+    # The reference's attribute names for the world and the model path
+    # (python/zeno/__init__.py:49 documents env._world.get_body_positions(zero_copy=True)).
+    @property
+    def _world(self) -> ZenoWorld:
+        return self.world
+
+    @property
+    def _mjcf_path(self) -> Optional[str]:
+        return self.mjcf_path
 
     # ---- sizes ------------------------------------------------------------------------------
     @property
