@@ -1,14 +1,16 @@
 """The step kernel divides several fp32 numbers by one divisor through one fp64 reciprocal
-(v_rcp_f64 and a cubic correction, then fp32(a * y); `rcp64` / `div_r` in dmath.h), which must
-give the bits of the IEEE fp32 division the reference and the oracle evaluate. The same device
-code, through zeno_amd_selfcheck_divide, against numpy's fp32 division: every significand of
-the numerator against a set of divisors (normal, subnormal, huge, negative), random bit
-patterns over the whole fp32 range, and the special values."""
+(v_rcp_f64 and a cubic correction, then fp32(a * y) with the subnormal tie rule; `rcp64` / `qdivs`
+in dmath.h), which must give the bits of the IEEE fp32 division the reference and the oracle
+evaluate. The same device code, through zeno_amd_selfcheck_divide, against numpy's fp32
+division: every significand of the numerator against a set of divisors (normal, subnormal,
+huge, negative), random bit patterns over the whole fp32 range, exact midpoints of the
+subnormal grid and their neighbours, and the special values."""
 import ctypes as C
 
 import numpy as np
 import pytest
 
+from tests.test_shared_reciprocal import subnormal_midpoints
 from zeno_amd import _lib
 
 pytestmark = pytest.mark.gpu
@@ -77,3 +79,13 @@ def test_reciprocal_error_over_every_divisor():
     err = C.c_double(-1.0)
     assert lib.zeno_amd_selfcheck_reciprocal_error(C.byref(err)) == 0, _lib.last_error()
     assert 0.0 < err.value <= 2.0**-52, err.value
+
+
+def test_subnormal_midpoints():
+    """Quotients exactly halfway between two fp32 subnormals round to the even one; their
+    neighbours (numerator one step up or down) are no ties."""
+    a, b = subnormal_midpoints(400_000, 31)
+    assert_same_bits(device_quotients(a, b), ieee_quotients(a, b), "subnormal midpoints")
+    for step in (-1, 1):
+        a2 = (a.view(np.int32) + step).view(np.float32)
+        assert_same_bits(device_quotients(a2, b), ieee_quotients(a2, b), f"midpoint neighbours {step}")

@@ -1,5 +1,5 @@
 """The step kernel divides several fp32 numbers by one divisor through a single fp64
-reciprocal (`rcp64` / `div_r` in zeno_amd/csrc/dmath.h: y = 1/b from v_rcp_f64 and its cubic
+reciprocal (`rcp64` / `qdivs` in zeno_amd/csrc/dmath.h: y = 1/b from v_rcp_f64 and its cubic
 correction, then each quotient is fp32(fp64(a * y))). Its results must be the bits of the fp32
 division a / b that the reference and the oracle evaluate. This checks that property of the
 arithmetic on the CPU (numpy's float32 division and float64 product are IEEE, round to nearest
@@ -12,14 +12,35 @@ code itself over the same operands.
 import numpy as np
 
 
-def shared_reciprocal_quotients(a: np.ndarray, b: np.ndarray, ulps: np.ndarray) -> np.ndarray:
-    """The kernel's recipe with a reciprocal that is `ulps` fp64 ulps away from 1/b."""
+def shared_reciprocal_quotients(a: np.ndarray, b: np.ndarray, ulps: np.ndarray, snap: bool = True) -> np.ndarray:
+    """The kernel's recipe with a reciprocal that is `ulps` fp64 ulps away from 1/b: q = a * y
+    in fp64; |q| rounded to a multiple of 2^-176 by adding and subtracting 1.5 * 2^-124, the
+    sign copied back; then rounded to fp32."""
     b64 = b.astype(np.float64)
-    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore", under="ignore"):
         raw = 1.0 / b64
         y = (raw.view(np.int64) + ulps.astype(np.int64)).view(np.float64)
         y = np.where(np.isfinite(b) & (b != 0), y, raw)
-        return (a.astype(np.float64) * y).astype(np.float32)
+        q = a.astype(np.float64) * y
+        if snap:
+            C = 1.5 * 2.0**-124
+            q = np.copysign((np.abs(q) + C) - C, q)
+        return q.astype(np.float32)
+
+
+def subnormal_midpoints(n: int, seed: int):
+    """(a, b) whose exact quotient a / b is a midpoint of two adjacent fp32 subnormals (or of 0
+    and the smallest one): a = M B 2^(k-150), b = B 2^k with M, B odd, both exact in fp32."""
+    rng = np.random.default_rng(seed)
+    M = rng.integers(0, 2**11, n) * 2 + 1
+    B = rng.integers(0, 2**11, n) * 2 + 1
+    k = rng.integers(-20, 100, n)
+    a = (M * B).astype(np.float64) * 2.0 ** (k - 150)
+    b = B.astype(np.float64) * 2.0 ** k
+    sign = np.where(rng.random(n) < 0.5, -1.0, 1.0)
+    a32, b32 = (sign * a).astype(np.float32), b.astype(np.float32)
+    exact = (np.abs(a32.astype(np.float64)) == a) & (b32.astype(np.float64) == b)
+    return a32[exact], b32[exact]
 
 
 def assert_same_bits(got: np.ndarray, want: np.ndarray):
@@ -81,3 +102,50 @@ def test_special_values():
     a, b = a.reshape(-1), b.reshape(-1)
     for k in (-4, 0, 4):
         assert_same_bits(shared_reciprocal_quotients(a, b, np.full(a.size, k)), fp32_quotients(a, b))
+
+
+def test_subnormal_midpoint_quotients():
+    """Exact ties exist only for subnormal quotients (a normal quotient's midpoint needs a
+    25-bit odd significand times B, more bits than a holds). Without the even-divisor rule the
+    fp64 product lands on either side of the midpoint and rounds the wrong way for many. The
+    device's reciprocal is within one fp64 ulp of 1/b (|1 - b y| <= 2^-53 over every divisor),
+    so q is within 2^-178 of a tie and the snap to the 2^-176 grid lands on it."""
+    a, b = subnormal_midpoints(400_000, 21)
+    assert a.size > 100_000
+    want = fp32_quotients(a, b)
+    for k in (-1, 0, 1):
+        ulps = np.full(a.size, k)
+        assert_same_bits(shared_reciprocal_quotients(a, b, ulps), want)
+    plain = shared_reciprocal_quotients(a, b, np.full(a.size, 1), snap=False)
+    assert np.count_nonzero(plain.view(np.uint32) != want.view(np.uint32)) > 1000
+
+
+def test_every_tie_has_an_even_integer_divisor():
+    """Brute force over small cases: for every odd numerator significand M*2^-149 (M < 2^12)
+    and every divisor B*2^e (B < 2^8, e in -8..8), the quotient is an exact fp32 rounding tie
+    (an odd multiple of 2^-150, checked in exact integer arithmetic) only when the divisor is
+    an even integer; ties are rare operand pairs, not a rounding artefact of the model."""
+    from fractions import Fraction
+    ties = 0
+    for B in range(1, 256, 2):
+        for e in range(-8, 9):
+            bq = Fraction(B) * Fraction(2) ** e
+            for M in range(1, 1 << 12, 2):
+                t = Fraction(M, 1) * Fraction(1, 2 ** 149) / bq   # a / b exactly
+                u = t * 2 ** 150                                      # in half-spacings
+                if u.denominator == 1 and u.numerator % 2 == 1:
+                    ties += 1
+                    assert bq.denominator == 1 and bq.numerator % 2 == 0, (M, B, e)
+    assert ties > 1000
+
+
+def test_snap_leaves_near_midpoints_alone():
+    """Quotients one fp32 step of a away from an exact midpoint are no ties: at least 2^-174
+    from any midpoint, so neither the reciprocal's error nor the snap moves them across."""
+    a, b = subnormal_midpoints(200_000, 22)
+    for step in (-1, 1):
+        a2 = (a.view(np.int32) + step).view(np.float32)
+        ok = np.isfinite(a2) & (np.sign(a2) == np.sign(a))
+        want = fp32_quotients(a2[ok], b[ok])
+        for k in (-4, 0, 4):
+            assert_same_bits(shared_reciprocal_quotients(a2[ok], b[ok], np.full(ok.sum(), k)), want)

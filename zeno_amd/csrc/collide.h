@@ -18,7 +18,7 @@ hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAm
                                           ZenoAmdContactResult* out);
 
 // q[i] = a[i] / b[i] through the step kernel's shared-reciprocal division (dmath.h rcp64 and
-// div_r) on host arrays: copies in, runs on the current device, copies back, waits.
+// qdivs) on host arrays: copies in, runs on the current device, copies back, waits.
 hipError_t selfcheck_divide_host(const float* a, const float* b, float* q, uint32_t n);
 hipError_t selfcheck_sqrt_host(const float* x, float* y, uint32_t n);
 hipError_t selfcheck_rcp_error_host(double* max_err);

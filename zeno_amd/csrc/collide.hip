@@ -173,7 +173,8 @@ hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAm
 namespace {
 __global__ __launch_bounds__(256) void selfcheck_divide_kernel(const float* a, const float* b, float* q, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) q[i] = div_r(a[i], rcp64(b[i]));
+    // The step kernel's four-quotient path (qdivs), with neighbouring lanes of the operand.
+    if (i < n) q[i] = qdivs(q4{a[i], 0.0f, -a[i], a[i]}, b[i]).w;
 }
 // max |1 - b rcp64(b)| over the fp32 bit patterns [base, base + 2^32 / gridDim.x ...): each
 // thread takes 256 consecutive patterns; a wave reduces its lanes and one lane folds the wave's

@@ -21,19 +21,24 @@ __device__ __forceinline__ f3 sub(f3 a, f3 b) { return {a.x - b.x, a.y - b.y, a.
 __device__ __forceinline__ f3 mul(f3 a, f3 b) { return {a.x * b.x, a.y * b.y, a.z * b.z}; }
 __device__ __forceinline__ f3 scale(f3 a, float s) { return {a.x * s, a.y * s, a.z * s}; }
 __device__ __forceinline__ f3 sscale(float s, f3 a) { return {s * a.x, s * a.y, s * a.z}; }
-// Several fp32 quotients with one divisor, through one fp64 reciprocal. For fp32 a and b the
-// exact quotient a / b is either an fp32 number or at least 2^-49 (relative) away from every
-// rounding boundary of the fp32 grid: with a = A 2^ea, b = B 2^eb (A, B < 2^24) and a boundary
-// m = M 2^em (M odd, < 2^25), a - m b is a nonzero multiple of 2^(em+eb), so
-// |a / b - m| >= 2^-49 m. y = 1 / b is the v_rcp_f64 estimate r0 refined by the cubic
-// correction r0 (1 + e + e^2), e = 1 - b r0 (three dependent fp64 FMAs; the relative error
-// becomes about e^3 plus one rounding). Over every finite nonzero fp32 b, |1 - b r0| <= 2^-24.39
-// and |1 - b y| <= 2^-53 (measured exhaustively on gfx950: zeno_amd_selfcheck_reciprocal_error);
-// a * y rounded to fp64 is then within ~2^-52 of a / b, on
-// the same side of every boundary, so its rounding to fp32 is the correctly rounded a / b (the
-// bits of the fp32 division, subnormal and overflowing quotients included: the fp64 range holds
-// every fp32 quotient). A zero or infinite divisor keeps the raw reciprocal (+-inf, +-0, exact),
-// so a * y gives the IEEE quotient (+-inf, +-0 or NaN); a NaN divisor gives NaN.
+// Several fp32 quotients with one divisor, through one fp64 reciprocal. y = 1 / b is the
+// v_rcp_f64 estimate r0 refined by the cubic correction r0 (1 + e + e^2), e = 1 - b r0 (three
+// dependent fp64 FMAs; the relative error becomes about e^3 plus one rounding). Over every
+// finite nonzero fp32 b, |1 - b r0| <= 2^-24.39 and |1 - b y| <= 2^-53 (measured exhaustively
+// on gfx950: zeno_amd_selfcheck_reciprocal_error), so q = fp64(a * y) is within ~2^-52 of a / b.
+//
+// Why fp32(q) is the correctly rounded a / b. Write a = A 2^ea, b = B 2^eb (A, B < 2^24
+// integers) and let m = M 2^em be a rounding boundary of the fp32 grid (a midpoint of two
+// neighbours, M odd). If a / b != m, then a - m b is a nonzero multiple of 2^min(ea, em+eb),
+// which puts a / b at least 2^-50 (relative to m) away from m; q, within 2^-52, lies on the
+// same side of every boundary, and its rounding is that of a / b. A quotient exactly at a
+// boundary (a = m b) needs A = M B 2^j: for a normal quotient M has 25 bits, more than A holds,
+// so this cannot happen; for a subnormal quotient the boundaries are the odd multiples of
+// 2^-150 and small M make exact ties possible (a = 147 2^-149, b = 98), where q, off the tie
+// by its error, would round to either side; to_f32_tie_even settles them. Overflowing quotients
+// land beyond the fp32 range of q and convert to infinity. A zero or infinite divisor keeps the
+// raw reciprocal (+-inf, +-0, exact), so a * y gives the IEEE quotient (+-inf, +-0 or NaN); a
+// NaN divisor gives NaN.
 __device__ __forceinline__ double rcp64(float b) {
     const double d = (double)b;
     const double r0 = __builtin_amdgcn_rcp(d);
@@ -41,10 +46,27 @@ __device__ __forceinline__ double rcp64(float b) {
     const double r = __builtin_fma(r0, __builtin_fma(e, e, e), r0);
     return (__builtin_isfinite(b) && b != 0.0f) ? r : r0;
 }
-__device__ __forceinline__ float div_r(float a, double y) { return (float)((double)a * y); }
+// fp32(q) for q = fp64(a * y). |q| is first rounded to a multiple of 2^-176 by adding and
+// subtracting C = 1.5 2^-124 (both exact-rounding fp64 operations; -fno-fast-math keeps them):
+// for |q| < 2^-125 the sum lies in [2^-124, 2^-123), where the spacing is 2^-176, and the
+// subtraction is exact; for |q| >= 2^-71 both operations give q back unchanged; in between
+// they move q by at most 2^-52 relative. A subnormal tie sits within 2^-177.4 of its midpoint,
+// an odd multiple of 2^-150, and lands on it exactly; every other subnormal quotient is at
+// least 2^-174 from a midpoint and keeps its side. The fp32 conversion then rounds a tie to
+// even, as IEEE division does. The sign is copied back so that -0 stays -0.
+__device__ __forceinline__ float to_f32_tie_even(double q) {
+    constexpr double C = 0x1.8p-124;
+    return (float)__builtin_copysign((__builtin_fabs(q) + C) - C, q);
+}
 __device__ __forceinline__ f3 divs(f3 a, float s) {
     const double y = rcp64(s);
-    return {div_r(a.x, y), div_r(a.y, y), div_r(a.z, y)};
+    return {to_f32_tie_even((double)a.x * y), to_f32_tie_even((double)a.y * y), to_f32_tie_even((double)a.z * y)};
+}
+// q / l for the four components, through one reciprocal (see divs).
+__device__ __forceinline__ q4 qdivs(q4 q, float l) {
+    const double y = rcp64(l);
+    return {to_f32_tie_even((double)q.x * y), to_f32_tie_even((double)q.y * y),
+            to_f32_tie_even((double)q.z * y), to_f32_tie_even((double)q.w * y)};
 }
 __device__ __forceinline__ f3 neg(f3 a) { return {-a.x, -a.y, -a.z}; }
 __device__ __forceinline__ float dot(f3 a, f3 b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
@@ -96,15 +118,13 @@ __device__ __forceinline__ float qlen(q4 q) { return __builtin_sqrtf(q.x * q.x +
 __device__ __forceinline__ q4 qnormalize(q4 q) {
     const float l = qlen(q);
     if (!(l > 1e-8f)) return q4{0.0f, 0.0f, 0.0f, 1.0f};
-    const double y = rcp64(l);  // q / l with one reciprocal (see divs)
-    return q4{div_r(q.x, y), div_r(q.y, y), div_r(q.z, y), div_r(q.w, y)};
+    return qdivs(q, l);
 }
 // qnormalize with the quotients evaluated before the length test and the identity selected
 // after it (same results; sqrt_gate is exact wherever the test l > 1e-8 passes).
 __device__ __forceinline__ q4 qnormalize_sel(q4 q) {
     const float l = sqrt_gate(q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w);
-    const double y = rcp64(l);
-    const q4 r{div_r(q.x, y), div_r(q.y, y), div_r(q.z, y), div_r(q.w, y)};
+    const q4 r = qdivs(q, l);
     return l > 1e-8f ? r : q4{0.0f, 0.0f, 0.0f, 1.0f};
 }
 // Quaternion step q + s * ((d, 0) (x) q) used by every XPBD rotation update.
