@@ -112,9 +112,10 @@ int zeno_amd_world_split_groups(ZenoWorldHandle world);
 
 /* *placement: where the step kernel keeps the scene's model records and each environment's
  * working set. 0 = both in LDS (several environments per workgroup); 1 = model records read
- * from HBM, working set in LDS; 2 = both in HBM. The world picks the one that keeps the
- * most environments resident on the GPU (HIP occupancy query); ZENO_AMD_PLACEMENT=0/1/2
- * at create forces one.
+ * from HBM, working set in LDS; 2 = both in HBM, the contact pipeline's arrays in LDS; 3 = all
+ * in HBM, no LDS (contact lists too long for LDS). The world picks, among 0-2, the one that
+ * keeps the most environments resident on the GPU (HIP occupancy query), and 3 when none of
+ * them fits; ZENO_AMD_PLACEMENT=0/1/2/3 at create forces one.
  * *spatial_hash = 1 when the scene has more than 512 geoms and the spatial-hash broad
  * phase runs (world.zig:534, all_shaders.metal:541-703). Either pointer may be null. */
 int zeno_amd_world_modes(ZenoWorldHandle world, int* placement, int* spatial_hash);

@@ -47,19 +47,6 @@ def test_mode_is_off_by_default_and_switchable():
     compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
 
 
-def test_contact_list_beyond_lds_is_rejected():
-    """pile_hash (601 bodies) at max_contacts_per_env=2048 needs more LDS per environment than
-    a workgroup has even with the working set and the slot masks in HBM (the contact records
-    alone are 128 KB): world creation fails with the sizes."""
-    with pytest.raises(RuntimeError, match="LDS working set"):
-        make_pair("pile_hash", 2, 1, max_contacts=2048)
-    # the failed shape queries leave no error behind for the next world
-    g, o, acts = make_pair("pile", 2, 1, seed=7)
-    g.step(acts[0])
-    o.step(acts[0])
-    compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
-
-
 def test_extended_mode_switches_to_the_grouped_shape_and_back():
     """A placement-0 world with a long contact list runs the extended mode in the
     one-environment-per-wave shape without split groups (the type-grouped narrow phase) and

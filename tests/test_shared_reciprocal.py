@@ -121,21 +121,23 @@ def test_subnormal_midpoint_quotients():
 
 
 def test_every_tie_has_an_even_integer_divisor():
-    """Brute force over small cases: for every odd numerator significand M*2^-149 (M < 2^12)
-    and every divisor B*2^e (B < 2^8, e in -8..8), the quotient is an exact fp32 rounding tie
-    (an odd multiple of 2^-150, checked in exact integer arithmetic) only when the divisor is
-    an even integer; ties are rare operand pairs, not a rounding artefact of the model."""
-    from fractions import Fraction
+    """Brute force over small cases: for every odd numerator significand M 2^-149 (M < 2^13)
+    and every divisor B 2^e (B odd < 2^9, e in -12..12), the quotient is an exact fp32 rounding
+    tie (an odd multiple of 2^-150: u = a / b 2^150 = 2M / (B 2^e) an odd integer, checked in
+    integer arithmetic) only when the divisor is an even integer. Ties are rare operand pairs,
+    not an artefact of the model."""
+    M = np.arange(1, 1 << 13, 2, dtype=np.int64)[:, None]
+    B = np.arange(1, 1 << 9, 2, dtype=np.int64)[None, :]
     ties = 0
-    for B in range(1, 256, 2):
-        for e in range(-8, 9):
-            bq = Fraction(B) * Fraction(2) ** e
-            for M in range(1, 1 << 12, 2):
-                t = Fraction(M, 1) * Fraction(1, 2 ** 149) / bq   # a / b exactly
-                u = t * 2 ** 150                                      # in half-spacings
-                if u.denominator == 1 and u.numerator % 2 == 1:
-                    ties += 1
-                    assert bq.denominator == 1 and bq.numerator % 2 == 0, (M, B, e)
+    for e in range(-12, 13):
+        if e <= 1:
+            num, den = M << (1 - e), B          # u = num / den
+        else:
+            num, den = M, B << (e - 1)
+        tie = (num % den == 0) & ((num // den) % 2 == 1)
+        even_integer_divisor = e >= 1           # B 2^e with B odd is an even integer iff e >= 1
+        assert not tie.any() or even_integer_divisor, e
+        ties += int(tie.sum())
     assert ties > 1000
 
 

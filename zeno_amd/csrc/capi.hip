@@ -430,7 +430,8 @@ int zeno_amd_world_launch_config(ZenoWorldHandle world, uint32_t* envs_per_wave,
     const World* w = W(world);
     if (envs_per_wave) *envs_per_wave = (uint32_t)w->epw;
     if (lds_bytes) {
-        *lds_bytes = w->placement == za::PL_ALL_HBM ? w->lds_small.bytes
+        *lds_bytes = w->placement == za::PL_WORK_HBM ? 0u
+                   : w->placement == za::PL_ALL_HBM ? w->lds_small.bytes
                    : w->lds.bytes * (uint32_t)(w->epw * w->waves) + (w->placement == za::PL_LDS ? w->ml.bytes : 0u);
     }
     return ZENO_SUCCESS;

@@ -64,13 +64,15 @@ inline uint32_t hash_bytes_for(uint32_t G, bool staged) {
 }
 
 // G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
-// solve records when they are copied per environment (HBM working set), else 0.
+// solve records when they are copied per environment (HBM working set), else 0;
+// hash_staged: the spatial hash's staged geom centres and metadata (hpos / hmeta) are part of
+// the layout (a working set whose contact arrays live in HBM as well, placement 3).
 inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint32_t G = 0, uint32_t jrec_bytes = 0,
-                           bool stage_geoms = false, uint32_t obsp = 1) {
+                           bool stage_geoms = false, uint32_t obsp = 1, bool hash_staged = false) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
-    const uint32_t hash_bytes = hash_bytes_for(G, false);
+    const uint32_t hash_bytes = hash_bytes_for(G, hash_staged);
     L.pos = take(16 * B); L.quat = take(16 * B); L.vel = take(16 * B); L.angvel = take(16 * B);
     L.ppos = take(16 * B); L.pquat = take(16 * B); L.frc = take(16 * B); L.trq = take(16 * B);
     L.vbefore = take(16 * B);
@@ -84,7 +86,9 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
     L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
-    L.hpos = L.skey;  // unused: the queries stage nothing when the working set is in LDS
+    // The queries stage nothing when the working set is in LDS; in HBM (placement 3) they
+    // stage each geom's centre and metadata after the sorted keys and cells.
+    L.hpos = L.skey + (hash_staged && G > kHashMinGeoms ? hash_hpos_off(G) : 0);
     // Per-body bit masks of the valid contact slots touching the body (u64[B][ceil(M/64)]),
     // on the force and torque arrays (dead from integration to the next substep) when they fit.
     const uint32_t mask_words = (M + 63) / 64;
@@ -334,7 +338,7 @@ struct StepArgs {
     unsigned long long* phase_ticks; // [kPhaseCount]
     uint32_t* cell_ids;             // [E*G] hash mode: each geom's cell in the last substep
     uint32_t placement;             // Placement of the model records and working sets
-    unsigned char* work;            // PL_ALL_HBM: lds.bytes per environment; else null
+    unsigned char* work;            // PL_ALL_HBM, PL_WORK_HBM: lds.bytes per environment; else null
     EnvLds lds;
     EnvLds lds_small;               // PL_ALL_HBM: the arrays kept in LDS (make_env_lds_small)
 };
@@ -342,8 +346,11 @@ struct StepArgs {
 // Where the step kernel keeps the model records and each environment's working set.
 // PL_LDS: both in LDS (several environments per workgroup). PL_MODEL_HBM: the model blob
 // is read in place from HBM (through the caches) and the working set is in LDS.
-// PL_ALL_HBM: both in HBM. The world picks the first that fits a workgroup's LDS.
-enum Placement : uint32_t { PL_LDS = 0, PL_MODEL_HBM = 1, PL_ALL_HBM = 2 };
+// PL_ALL_HBM: both in HBM, except the contact pipeline's arrays (make_env_lds_small), which
+// stay in LDS. PL_WORK_HBM: everything in HBM, for contact lists too long for LDS
+// (max_contacts_per_env beyond ~1,400: 64-B records, snapshot and sort keys are ~104 B per
+// slot); the kernel then uses no LDS. The world scores the shapes that fit and keeps the best.
+enum Placement : uint32_t { PL_LDS = 0, PL_MODEL_HBM = 1, PL_ALL_HBM = 2, PL_WORK_HBM = 3 };
 
 // Phases timed by the kernel when profiling is enabled.
 enum Phase { PH_LOAD, PH_FORCES, PH_BROAD, PH_NARROW, PH_JOINTS, PH_CONTACTS, PH_POST, PH_STORE, kPhaseCount };

@@ -739,7 +739,9 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
 // PL: where the model records and the working sets live (Placement): PL_LDS, both in LDS
 // (EPW environments per wave, and up to kMaxWaves independent waves per workgroup sharing one
 // copy of the model records); PL_MODEL_HBM, the model blob read in place from HBM and one
-// working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work).
+// working set in LDS; PL_ALL_HBM, both in HBM (the working set in a.work) but the contact
+// pipeline's arrays in LDS; PL_WORK_HBM, all of it in HBM (no LDS), for contact lists longer
+// than LDS holds.
 // HASH: the spatial-hash broad phase (scenes above kHashMinGeoms geoms) instead of the
 // candidate pair list. Both non-LDS placements and the hash run one environment per
 // workgroup. GROUP: the narrow phase visits the slots grouped by geom-type pair (the
@@ -763,7 +765,7 @@ __global__ __launch_bounds__(SPLIT ? 2 * kMaxWaves * kWave : (PL == PL_LDS && !H
 __attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
-    constexpr bool HBM = PL == PL_ALL_HBM;  // working set in HBM
+    constexpr bool HBM = PL >= PL_ALL_HBM;  // working set in HBM
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     static_assert(!GROUP || EPW == 1, "type-grouped narrow phase: one environment per workgroup");
@@ -785,7 +787,7 @@ void step_kernel(StepArgs a) {
     unsigned char* const env_base = HBM ? a.work + (size_t)wave_id * a.lds.bytes
                                         : smem + (PL == PL_LDS ? a.ml.bytes : 0u) + grp * EPW * a.lds.bytes;
     Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
-    if (HBM) bind_small(s, smem, a.lds_small);
+    if (PL == PL_ALL_HBM) bind_small(s, smem, a.lds_small);  // PL_WORK_HBM: all of it in a.work
     bind_levels(s, a.M);
     Mdl md = bind_model(PL == PL_LDS ? smem : (const unsigned char*)a.model, a.ml);
     if (PL != PL_LDS) md.jrec = s.jrec;
@@ -1929,6 +1931,7 @@ int resident_workgroups(int envs_per_wave, uint32_t placement, bool hash, size_t
             case PL_LDS: return resident_as<1, PL_LDS, true>(shmem);
             case PL_MODEL_HBM: return hash ? resident_as<1, PL_MODEL_HBM, true>(shmem) : resident_as<1, PL_MODEL_HBM, false>(shmem);
             case PL_ALL_HBM: return hash ? resident_as<1, PL_ALL_HBM, true>(shmem) : resident_as<1, PL_ALL_HBM, false>(shmem);
+            case PL_WORK_HBM: return hash ? resident_as<1, PL_WORK_HBM, true>(shmem) : resident_as<1, PL_WORK_HBM, false>(shmem);
             default: return 0;
         }
     }
@@ -1957,13 +1960,16 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStrea
     const uint32_t per_group = (uint32_t)envs_per_wave * (uint32_t)waves;
     const uint32_t blocks = (a.E + per_group - 1) / per_group;
     if ((a.placement != PL_LDS || a.hash) && (envs_per_wave != 1 || waves != 1)) return hipErrorInvalidValue;
-    if ((a.placement == PL_ALL_HBM) != (a.work != nullptr)) return hipErrorInvalidValue;
+    if ((a.placement >= PL_ALL_HBM) != (a.work != nullptr)) return hipErrorInvalidValue;
     const size_t env_lds = (size_t)a.lds.bytes * (size_t)envs_per_wave;
     const size_t shmem = (size_t)a.ml.bytes + env_lds * (size_t)waves;
     // Extended-contact mode with one environment per workgroup: the instance whose narrow
     // phase visits the slots grouped by geom-type pair (same results, less divergence).
     if (a.ext_contacts && a.M >= 64 && envs_per_wave == 1 && !split) {
         switch (a.placement) {
+            case PL_WORK_HBM:
+                return a.hash ? launch_as<1, PL_WORK_HBM, true, true>(a, blocks, 0, stream)
+                              : launch_as<1, PL_WORK_HBM, false, true>(a, blocks, 0, stream);
             case PL_ALL_HBM:
                 return a.hash ? launch_as<1, PL_ALL_HBM, true, true>(a, blocks, a.lds_small.bytes, stream)
                               : launch_as<1, PL_ALL_HBM, false, true>(a, blocks, a.lds_small.bytes, stream);
@@ -1977,6 +1983,9 @@ hipError_t launch_step(const StepArgs& a, int envs_per_wave, int waves, hipStrea
         }
     }
     switch (a.placement) {
+        case PL_WORK_HBM:
+            return a.hash ? launch_as<1, PL_WORK_HBM, true>(a, blocks, 0, stream)
+                          : launch_as<1, PL_WORK_HBM, false>(a, blocks, 0, stream);
         case PL_ALL_HBM:
             return a.hash ? launch_as<1, PL_ALL_HBM, true>(a, blocks, a.lds_small.bytes, stream)
                           : launch_as<1, PL_ALL_HBM, false>(a, blocks, a.lds_small.bytes, stream);

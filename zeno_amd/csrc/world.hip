@@ -183,7 +183,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     // the second running the contact pipeline (broad phase to contact levels) while the first
     // solves the joints; same LDS, twice the waves (Ant 4096 74.4 -> 66.2 us per step,
     // Humanoid 16384 266 -> 232 us).
-    // ZENO_AMD_PLACEMENT=0/1/2, ZENO_AMD_ENVS_PER_WAVE, ZENO_AMD_WAVES and ZENO_AMD_SPLIT=0/1
+    // ZENO_AMD_PLACEMENT=0/1/2/3, ZENO_AMD_ENVS_PER_WAVE, ZENO_AMD_WAVES and ZENO_AMD_SPLIT=0/1
     // force a placement or a shape (tests of each path; a forced shape implies placement 0).
     const size_t lds_max = max_lds_per_workgroup(w->device);
     int cus = 256;
@@ -195,10 +195,13 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         L_small = make_env_lds_small(w->B, w->Jp, std::max<uint32_t>(w->M, 1), m.num_geoms, !w->hash, false);
     const EnvLds L_own = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms, 16 * kJRecQuads * w->nrec,
                                       !w->hash, w->obsp);
+    // Placement 3: the whole working set in HBM, the hash's staged geoms included.
+    const EnvLds L_work = make_env_lds(w->B, w->Jp, w->N, std::max<uint32_t>(w->M, 1), m.num_geoms,
+                                       16 * kJRecQuads * w->nrec, !w->hash, w->obsp, true);
     struct Cand { uint32_t pl; int epw; int waves; size_t shmem; bool split; };
     std::vector<Cand> cands;
     int force_pl = -1, force_epw = 0, force_waves = 0, force_split = -1;
-    if (const char* env = std::getenv("ZENO_AMD_PLACEMENT")) force_pl = std::min(std::max(std::atoi(env), 0), 2);
+    if (const char* env = std::getenv("ZENO_AMD_PLACEMENT")) force_pl = std::min(std::max(std::atoi(env), 0), 3);
     if (const char* env = std::getenv("ZENO_AMD_ENVS_PER_WAVE")) force_epw = std::atoi(env);
     if (const char* env = std::getenv("ZENO_AMD_WAVES")) force_waves = std::atoi(env);
     if (const char* env = std::getenv("ZENO_AMD_SPLIT")) force_split = std::atoi(env) != 0 ? 1 : 0;
@@ -229,9 +232,14 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         if ((size_t)L_own.bytes <= lds_max) cands.push_back({PL_MODEL_HBM, 1, 1, (size_t)L_own.bytes, false});
         cands.push_back({PL_ALL_HBM, 1, 1, (size_t)L_small.bytes, false});
     }
+    // Placement 3 (no LDS at all) is the fallback for contact lists that no LDS layout
+    // holds: it scores well on residency, but its contact pipeline runs out of the caches.
+    const std::vector<Cand> fallback{{PL_WORK_HBM, 1, 1, 0, false}};
     const Cand* best = nullptr;
     uint64_t best_score = 0;
-    for (const Cand& c : cands) {
+    for (int pass = 0; pass < 2 && !best; ++pass) {
+      const std::vector<Cand>& list = pass == 0 ? cands : fallback;
+      for (const Cand& c : list) {
         if (force_pl >= 0 && (int)c.pl != force_pl) continue;
         if (force_epw > 0 && c.epw != force_epw) continue;
         if (force_waves > 0 && c.waves != force_waves) continue;
@@ -240,18 +248,18 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         if (n <= 0) continue;
         const uint64_t score = std::min<uint64_t>(w->E, (uint64_t)n * (uint64_t)c.epw * (uint64_t)c.waves * (uint64_t)cus);
         if (!best || score > best_score) { best = &c; best_score = score; }
+      }
     }
     if (!best) {
-        err = "no launch shape fits this scene: the smallest per-environment LDS working set is " +
-              std::to_string(L_small.bytes) + " bytes (contacts, sort keys, level masks for max_contacts_per_env=" +
-              std::to_string(w->M) + "), a workgroup may use " + std::to_string(lds_max) +
-              " (or ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE / ZENO_AMD_WAVES / ZENO_AMD_SPLIT force a shape that cannot launch)";
+        err = "no launch shape fits this scene (ZENO_AMD_PLACEMENT / ZENO_AMD_ENVS_PER_WAVE / ZENO_AMD_WAVES / "
+              "ZENO_AMD_SPLIT force a shape that cannot launch, or the step kernel cannot run on this device)";
         delete w;
         return nullptr;
     }
     w->placement = best->pl;
     const int epw = best->epw;
-    if (best->pl != PL_LDS) L = L_own;
+    if (best->pl == PL_MODEL_HBM || best->pl == PL_ALL_HBM) L = L_own;
+    if (best->pl == PL_WORK_HBM) L = L_work;
     w->lds = L;
     w->lds_small = L_small;
     w->epw = epw;
@@ -318,7 +326,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
     if ((e = dalloc(w, &w->d_counts, w->E)) != hipSuccess) return fail("hipMalloc", e);
     if ((e = dalloc(w, &w->d_pcounts, w->E)) != hipSuccess) return fail("hipMalloc", e);
     if (w->hash && (e = dalloc(w, &w->d_cell_ids, (size_t)w->E * m.num_geoms)) != hipSuccess) return fail("hipMalloc", e);
-    if (w->placement == PL_ALL_HBM && (e = dalloc(w, &w->d_work, (size_t)w->E * w->lds.bytes)) != hipSuccess) return fail("hipMalloc", e);
+    if (w->placement >= PL_ALL_HBM && (e = dalloc(w, &w->d_work, (size_t)w->E * w->lds.bytes)) != hipSuccess) return fail("hipMalloc", e);
     struct Z { void* p; size_t n; } zeros[] = {
         {w->d_pos, EB * 16}, {w->d_quat, EB * 16}, {w->d_vel, EB * 16}, {w->d_angvel, EB * 16}, {w->d_acc, EB * 16},
         {w->d_jpos, (size_t)w->E * w->Jp * 4}, {w->d_jvel, (size_t)w->E * w->Jp * 4}, {w->d_jtrq, (size_t)w->E * w->Jp * 4},

@@ -435,7 +435,8 @@ class ZenoWorld:
 
     def modes(self) -> Dict[str, Any]:
         """{"placement": 0 model + working sets in LDS, 1 model in HBM and working set in LDS,
-        2 both in HBM; "spatial_hash": the spatial-hash broad phase runs (G > 512)}."""
+        2 both in HBM with the contact pipeline's arrays in LDS, 3 everything in HBM (contact
+        lists too long for LDS); "spatial_hash": the spatial-hash broad phase runs (G > 512)}."""
         pl = C.c_int()
         sh = C.c_int()
         self._lib.zeno_amd_world_modes(self._handle, C.byref(pl), C.byref(sh))
