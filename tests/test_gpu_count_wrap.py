@@ -32,3 +32,53 @@ def test_count_wrap_matches_oracle(name, envs):
         compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
     wrapped = o.contact_counts < near
     assert wrapped.any() and not wrapped.all()
+
+
+def _pair_from_mjcf(xml, envs):
+    from oracle.oracle import OracleWorld
+    from zeno_amd.model import load_model
+    from zeno_amd.world import ZenoWorld
+    m = load_model(mjcf_string=xml)
+    return m, ZenoWorld(mjcf_string=xml, num_envs=envs), OracleWorld(m, envs)
+
+
+def test_wrap_with_appends_out_of_key_order():
+    """A body with two geoms makes the broad phase append pairs out of key order
+    (tests/test_count_wrap.py shows the oracle's list after the wrap then differs from the
+    append order): with the count 1-6 appends below 2^32, the wrapped appends must be sorted."""
+    from tests.test_count_wrap import WITH_PLANE
+    m, g, o = _pair_from_mjcf(WITH_PLANE, 6)
+    near = (np.uint64(1 << 32) - np.arange(1, 7, dtype=np.uint64)).astype(np.uint32)
+    g.set_contact_counts(near)
+    o.contact_counts[:] = near
+    for _ in range(3):
+        g.step(np.zeros((6, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+    assert np.all(o.contact_counts < near)
+    g.close()
+
+
+def test_host_count_exposes_stale_slots():
+    """Slots a reset left behind, exposed again by a count the host sets on a step with no
+    appends: the step sorts them as the reference does (tests/test_count_wrap.py builds the
+    same sequence on the oracle and shows the exposed list is out of order)."""
+    from tests.test_count_wrap import NO_PLANE, stale_slot_sequence
+    m, g, o = _pair_from_mjcf(NO_PLANE, 2)
+
+    def step():
+        g.step(np.zeros((2, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+
+    def reset_to_state(p, q):
+        g.reset_to_state(p, q)
+        o.reset_to_state(p, q)
+
+    def set_counts(c):
+        g.set_contact_counts(c)
+        o.contact_counts[:] = c
+
+    stale_slot_sequence(2, m, reset_to_state, set_counts, step)
+    np.testing.assert_array_equal(g.get_contact_counts(), [5, 5])
+    g.close()

@@ -302,6 +302,9 @@ struct StepArgs {
     uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P, G, Gp;
     uint32_t hash;  // 1: spatial-hash broad phase (G > kHashMinGeoms), 0: candidate pair list
     uint32_t ext_contacts;  // 1: pairs the reference's narrow phase leaves invalid use detectCollision
+    // 1: sort the contact list in the first substep even if no append took a slot below M (the
+    // host changed the counts, exposing slots whose order the last sort did not cover).
+    uint32_t sort_all;
     uint32_t iters, substeps;
     // Scalars (SimParams, world.zig:35-56).
     float dt, inv_step, gx, gy, gz, restitution, baumgarte, slop;

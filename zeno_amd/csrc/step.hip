@@ -1222,10 +1222,14 @@ void step_kernel(StepArgs a) {
         // two; the slot breaks ties between equal keys, so the order is the stable one.
         {
             const uint32_t n = count < M ? count : M;
-            // The list changed iff this step's appends (slots count_before .. count - 1, in
-            // u32 arithmetic) took a slot below M: from below M, or by wrapping past 2^32
-            // (the count is never cleared), after which the appends restart at slot 0.
-            const bool wrote = count != count_before && (count_before < M || count < count_before);
+            // The reference sorts the first min(count, M) slots every substep; a list the last
+            // sort left in order changes only when this step's appends (slots count_before ..
+            // count - 1, in u32 arithmetic) took a slot below M: from below M, or by wrapping
+            // past 2^32 (the count is never cleared), after which the appends restart at slot 0.
+            // A count the host has set since the last step may expose slots that sort never
+            // covered, so the first substep after it sorts unconditionally.
+            const bool wrote = (a.sort_all != 0u && step == 0) ||
+                               (count != count_before && (count_before < M || count < count_before));
             const bool need = live && wrote && n > 1;
             const bool big = __ballot(need && n > (uint32_t)(kMaxRecsPerLane * G)) != 0ull;
             if (!big) {

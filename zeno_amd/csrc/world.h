@@ -44,6 +44,7 @@ struct World {
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
     uint32_t placement = PL_LDS;  // where the step kernel keeps model records and working sets
     bool ext_contacts = false;    // extended-contact mode (zeno_amd_world_set_extended_contacts)
+    bool resort = false;          // counts set by the host: the next launch sorts unconditionally
     hipStream_t stream = nullptr;
     size_t device_bytes = 0;
 

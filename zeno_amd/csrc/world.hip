@@ -387,6 +387,8 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.G = model.num_geoms; a.Gp = hash ? hash_pad(model.num_geoms) : 0; a.hash = hash ? 1u : 0u;
     a.cell_ids = d_cell_ids;
     a.ext_contacts = ext_contacts ? 1u : 0u;
+    a.sort_all = resort ? 1u : 0u;
+    resort = false;
     a.placement = placement;
     a.work = d_work;
     a.iters = iters; a.substeps = substeps;
@@ -636,6 +638,7 @@ hipError_t World::set_contact_counts(const uint32_t* counts) {
     ZA_TRY(hipSetDevice(device));
     ZA_TRY(hipMemcpyAsync(d_counts, counts, (size_t)E * 4, hipMemcpyHostToDevice, stream));
     ZA_TRY(hipStreamSynchronize(stream));
+    resort = true;  // the next step sorts every env's first min(count, M) slots
     mark_all_dirty();
     return refresh_views();
 }
