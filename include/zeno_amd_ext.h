@@ -195,16 +195,17 @@ int zeno_amd_detect_collisions_host(const ZenoAmdCollider* a, const ZenoAmdColli
  * (3 MiB on each GPU the library runs on, held until the process ends) instead of buffers
  * allocated per call, and nothing is allocated or freed. n above that limit returns
  * ZENO_INVALID_ARGUMENT. Runs on the current device and waits. Every call on one GPU shares
- * that GPU's array: calls that overlap on one GPU (from several host threads) race. */
+ * that GPU's array, so calls on one GPU from several host threads take turns: each holds a
+ * per-device lock from its first copy in until its results are back. */
 #define ZENO_AMD_NOALLOC_MAX_PAIRS 16384u
 int zeno_amd_detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAmdCollider* b, uint32_t n,
                                             ZenoAmdContactResult* out);
 
 /* No counterpart in the reference: a self-check of the device arithmetic the step relies on.
  * q[i] = a[i] / b[i] evaluated the way the step kernel divides several numbers by one divisor
- * (one fp64 reciprocal from v_rcp_f64 and its cubic correction, then fp32(a * y)), which must give
- * the bits of the IEEE fp32 division for every input. Host arrays; runs on the current
- * device and waits. */
+ * (one fp64 reciprocal from v_rcp_f64 and its cubic correction, then fp32(a * y) with exact
+ * subnormal ties rounded to even), which must give the bits of the IEEE fp32 division for
+ * every input. Host arrays; runs on the current device and waits. */
 int zeno_amd_selfcheck_divide(const float* a, const float* b, float* q, uint32_t n);
 
 /* No counterpart in the reference: a self-check of the device arithmetic the step relies on.

@@ -62,3 +62,36 @@ def test_no_alloc_rejects_batches_above_its_limit():
     assert "16384" in L.last_error()
     assert not out.view(np.uint8).any()
     assert _call(lib.zeno_amd_detect_collisions_host_noalloc, a, b, 0, out) == 0
+
+
+def test_concurrent_calls_take_turns():
+    """Two host threads call the entry point at once on the one GPU with different batches;
+    the per-device lock makes each call's copy in, launch and copy back one unit, so every
+    result equals the allocating entry point's (ctypes drops the GIL during the calls)."""
+    import threading
+    lib = L.load()
+    batches = [_pairs(n, seed) for n, seed in ((9000, 4), (12000, 5))]
+    wants = []
+    for a, b in batches:
+        w = np.zeros(len(a), CONTACT_RESULT_DTYPE)
+        assert _call(lib.zeno_amd_detect_collisions_host, a, b, len(a), w) == 0
+        wants.append(w)
+    errors = []
+
+    def worker(i):
+        a, b = batches[i]
+        for rep in range(20):
+            got = np.zeros(len(a), CONTACT_RESULT_DTYPE)
+            rc = _call(lib.zeno_amd_detect_collisions_host_noalloc, a, b, len(a), got)
+            if rc != 0 or got.tobytes() != wants[i].tobytes():
+                errors.append((i, rep, rc))
+                return
+
+    print("no-alloc collide: two threads x 20 calls", flush=True)
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors

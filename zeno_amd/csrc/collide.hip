@@ -128,9 +128,13 @@ static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 
 constexpr int kMaxDevices = 64;
 
-// Device address of `scratch` on the current device, looked up once per device with that
-// device current.
-hipError_t scratch_on_current_device(unsigned char** out) {
+// One lock per device: a call holds its device's lock from the first copy into `scratch`
+// until its results are back, so calls from several host threads on one GPU take turns.
+std::mutex device_lock[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up once per device with that
+// device current) and the device's index.
+hipError_t scratch_on_current_device(unsigned char** out, int* device) {
     static std::mutex mu;
     static void* addr[kMaxDevices] = {};
     int dev = 0;
@@ -146,6 +150,7 @@ hipError_t scratch_on_current_device(unsigned char** out) {
         addr[dev] = p;
     }
     *out = static_cast<unsigned char*>(addr[dev]);
+    *device = dev;
     return hipSuccess;
 }
 
@@ -156,8 +161,10 @@ hipError_t detect_collisions_host_noalloc(const ZenoAmdCollider* a, const ZenoAm
     if (n == 0) return hipSuccess;
     if (n > kNoAllocPairs) return hipErrorInvalidValue;
     unsigned char* base = nullptr;
-    hipError_t e = scratch_on_current_device(&base);
+    int dev = 0;
+    hipError_t e = scratch_on_current_device(&base, &dev);
     if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> hold(device_lock[dev]);
     ZenoAmdCollider* da = reinterpret_cast<ZenoAmdCollider*>(base);
     ZenoAmdCollider* db = da + kNoAllocPairs;
     ZenoAmdContactResult* dout = reinterpret_cast<ZenoAmdContactResult*>(db + kNoAllocPairs);
