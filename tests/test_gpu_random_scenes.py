@@ -135,8 +135,8 @@ def _world(xml: str, envs: int, shape: dict) -> ZenoWorld:
 STABLE_SEEDS = [1, 2, 3, 4, 6, 8, 9]
 
 
-def _run_scene(rng: np.random.Generator, xml: str, shape: str) -> None:
-    E, steps = 13, 24  # an env count that leaves the last group partly empty
+def _run_scene(rng: np.random.Generator, xml: str, shape: str, steps: int = 24, finite: bool = True) -> None:
+    E = 13  # an env count that leaves the last group partly empty
     g = _world(xml, E, SHAPES[shape])
     o = OracleWorld(load_model(mjcf_string=xml), E)
     # Perturbed start: every env's bodies moved and spun a little, so contacts and limits
@@ -155,7 +155,11 @@ def _run_scene(rng: np.random.Generator, xml: str, shape: str) -> None:
         g.step(a)
         o.step(a)
         compare(gpu_arrays(g), oracle_arrays(o), **TOL)
-    assert np.isfinite(g.get_body_positions(zero_copy=False)).all()
+    ok = np.isfinite(g.get_body_positions(zero_copy=False)).all(axis=(1, 2))
+    if finite:
+        assert ok.all()
+    else:
+        assert not ok.all() and ok.any()  # some envs went non-finite, others did not
     g.close()
 
 
@@ -164,6 +168,22 @@ def _run_scene(rng: np.random.Generator, xml: str, shape: str) -> None:
 def test_random_scene_matches_oracle(seed, shape):
     rng = np.random.default_rng(1000 + seed)
     _run_scene(rng, random_scene_mjcf(rng), shape)
+
+
+# The seeds left out above blow up: positions reach 1e7 and velocities 1e10 within 24 steps,
+# and some environments overflow to inf and NaN after 55-58 steps. Run past that point, every
+# step compared: NaN poses go through the broad phase (a NaN distance passes the margin test),
+# the sort, the narrow phase, the contact levels and the solves, and the discrete outputs
+# (counts, pair lists, active flags) must stay exactly the oracle's, the fp32 state bit for
+# bit (any NaN matching any NaN).
+UNSTABLE_SEEDS = [0, 5, 7]
+
+
+@pytest.mark.parametrize("shape", ["auto", "one_env_per_wave", "split_epw4", "model_in_hbm"])
+@pytest.mark.parametrize("seed", UNSTABLE_SEEDS)
+def test_random_scene_through_non_finite_state(seed, shape):
+    rng = np.random.default_rng(1000 + seed)
+    _run_scene(rng, random_scene_mjcf(rng), shape, steps=64, finite=False)
 
 
 # Mixed joint ranges: seeds whose scenes stay finite over the run and hold both an angular limit
@@ -194,9 +214,23 @@ EXT_SEEDS = [1, 2, 4, 5, 8, 14]
 @pytest.mark.parametrize("shape", ["auto", "one_env_per_wave", "model_in_hbm"])
 @pytest.mark.parametrize("seed", EXT_SEEDS)
 def test_random_scene_extended_contacts_match_oracle(seed, shape):
+    _run_extended(seed, shape, steps=24, finite=True)
+
+
+# Extended-mode seeds that overflow to inf / NaN in some environments after 43-57 steps.
+EXT_UNSTABLE_SEEDS = [0, 6, 10]
+
+
+@pytest.mark.parametrize("shape", ["auto", "model_in_hbm"])
+@pytest.mark.parametrize("seed", EXT_UNSTABLE_SEEDS)
+def test_random_scene_extended_contacts_through_non_finite_state(seed, shape):
+    _run_extended(seed, shape, steps=64, finite=False)
+
+
+def _run_extended(seed: int, shape: str, steps: int, finite: bool) -> None:
     rng = np.random.default_rng(1000 + seed)
     xml = random_scene_mjcf(rng)
-    E, steps, M = 13, 24, 128
+    E, M = 13, 128
     saved = {k: os.environ.get(k) for k in SHAPES[shape]}
     try:
         os.environ.update(SHAPES[shape])
@@ -228,5 +262,6 @@ def test_random_scene_extended_contacts_match_oracle(seed, shape):
         live = np.arange(M)[None, :] < np.minimum(o.contact_counts, M)[:, None]
         active += int(((o.contacts["position_pen"][..., 3] >= 0) & live).sum())
     assert active > 0
-    assert np.isfinite(g.get_body_positions(zero_copy=False)).all()
+    ok = np.isfinite(g.get_body_positions(zero_copy=False)).all(axis=(1, 2))
+    assert ok.all() if finite else (not ok.all() and ok.any())
     g.close()
