@@ -73,6 +73,9 @@ def _cases():
         "spinner_world_frame": (P.SPINNER, (0, 0, 0), 4, 1, {1: dict(quat=qa90x, angvel=(0, 0, 3.0))}, None),
         "raised_plane": (P.RAISED_PLANE, None, 4, 1, {}, None),
         "two_geoms_one_body": (P.TWO_GEOMS_ONE_BODY, (0, 0, 0), 4, 1, {}, None),
+        "weld_dynamic_parent": (P.WELD_ON_FREE_PARENT, (0, 0, 0), 1, 1, {2: dict(pos=(0.3, 0.2, 1.0))}, None),
+        "angular_limit_lower": (P.HINGE_LIMIT, (0, 0, 0), 3, 1, {1: dict(quat=P._qaxis([0, 1, 0], -0.8))}, None),
+        "ball_driven_into_plane": (P.FALLING_BALL, (0, 0, 0), 1, 1, {1: dict(vel=(0.0, 0.0, -2.0))}, None),
     }
     ctrl = np.array([0.5, -0.05, 2e-6, 9e-7, -5e-7, 0.0, 1.0, -1.0], np.float32)
     for kind in ("hinge", "slide"):

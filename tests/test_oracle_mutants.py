@@ -162,10 +162,74 @@ MUTANTS = [
      "v3 v_pt_b = vadd(v_b, vcross(w_b, r_b));", "v3 v_pt_b = v_b;", 1),
     ("slide state: parent lever dropped from the velocity",
      "v3 v_pt_a = vadd(v_a, vcross(w_a, r_a));", "v3 v_pt_a = v_a;", 1),
-    # World.step (world.zig:736-746)
+    # World.step (world.zig:694-792)
     ("accelerations divided by the substep dt",
      "float inv_step = m->timestep > 0 ? 1.0f / m->timestep : 0.0f;",
      "float inv_step = dt > 0 ? 1.0f / dt : 0.0f;", 1),
+    ("substep dt not divided by the substep count",
+     "float dt = m->timestep / (float)div;", "float dt = m->timestep;", 1),
+    ("velocity snapshot taken every substep",
+     "        memcpy(pv, e.vel, sizeof(float) * 4 * B);\n"
+     "        for (uint32_t k = 0; k < actual; ++k) step_once(&e, act);",
+     "        for (uint32_t k = 0; k < actual; ++k) { memcpy(pv, e.vel, sizeof(float) * 4 * B); step_once(&e, act); }", 1),
+    # apply_actions (:196-229), apply_joint_forces (:122-190)
+    ("actions not clamped to the control range",
+     "float ctrl = clampf(actions[a], act->params[1], act->params[2]);", "float ctrl = actions[a];", 1),
+    ("torque not clamped to the force range",
+     "torque = clampf(torque, act->params2[0], act->params2[1]);", "(void)0;", 1),
+    ("slide joints take a torque",
+     "float* dst = type == 2 ? e->frc : e->trq;", "float* dst = e->trq;", 1),
+    # update_kinematic (:304-339), integrate (:394-462)
+    ("kinematic rotation without the half angle",
+     "v3 h = vscale(vscale(om, e->dt), 0.5f);", "v3 h = vscale(om, e->dt);", 1),
+    ("explicit Euler position (old velocity)",
+     "        vel = vadd(vel, vscale(accel, dt));\n"
+     "        vel = vscale(vel, 0.999f);\n"
+     "        pos = vadd(pos, vscale(vel, dt));",
+     "        pos = vadd(pos, vscale(vel, dt));\n"
+     "        vel = vadd(vel, vscale(accel, dt));\n"
+     "        vel = vscale(vel, 0.999f);", 1),
+    ("integration skips the quaternion renormalisation",
+     "if (ql > 1e-8f) quat = Q(quat.x / ql, quat.y / ql, quat.z / ql, quat.w / ql);",
+     "if (0) quat = Q(quat.x / ql, quat.y / ql, quat.z / ql, quat.w / ql);", 1),
+    # broad phase, sort (:711-745), narrow phase, match (:1483-1544)
+    ("planes take the distance test",
+     "            if (!is_plane_pair) {", "            if (1) {", 1),
+    ("sort not stable (equal keys move past each other)",
+     "if (j_val <= key_val) break;", "if (j_val < key_val) break;", 1),
+    ("sort key of the ordered pair (a, b) instead of (min, max)",
+     "uint32_t key_val = (ka << 16) | kb;",
+     "uint32_t key_val = (key.indices[0] << 16) | key.indices[1]; (void)ka; (void)kb;", 1),
+    ("capsule-plane depth of the shallower endpoint",
+     "float dist = fminf(d1, d2);", "float dist = fmaxf(d1, d2);", 1),
+    ("contact restitution not stored",
+     "c->impulses[3] = m->restitution;", "c->impulses[3] = 0.0f;", 1),
+    ("cache match radius inclusive",
+     "if (dsq < best) { best = dsq; best_i = (int)i; }", "if (dsq <= best) { best = dsq; best_i = (int)i; }", 1),
+    ("cache match scales the normal impulse by 0.9",
+     "c->impulses[0] = pc->impulses[0] * 0.8f;", "c->impulses[0] = pc->impulses[0] * 0.9f;", 1),
+    # solve_contacts (:1644-1793)
+    ("Baumgarte bias without the slop",
+     "float bias = beta * fmaxf(penetration - slop, 0.0f) / e->dt;", "float bias = beta * penetration / e->dt;", 1),
+    ("position correction without the slop",
+     "float pos_correction = beta * fmaxf(penetration - slop, 0.0f);", "float pos_correction = beta * penetration;", 1),
+    ("position correction split by the other body's inverse mass",
+     "float ratio = inv_mass_a / inv_mass_sum;", "float ratio = inv_mass_b / inv_mass_sum;", 1),
+    # solve_joints (:909-1399), lambda (:1427-1444)
+    ("lambda not stored for the next warm start",
+     "e->cs[i].state[1] = e->cs[i].state[0];", "(void)0;", 1),
+    ("hinge alignment with the opposite sign",
+     "float d_lambda = -ang_C / (w + alpha_tilde);", "float d_lambda = ang_C / (w + alpha_tilde);", 1),
+    ("angular limit violation with the opposite sign",
+     "if (angle < lower) violation = lower - angle;", "if (angle < lower) violation = angle - lower;", 1),
+    ("linear limit pushes the wrong way",
+     "v3 n = violation > 0 ? axis_world : vneg(axis_world);", "v3 n = violation > 0 ? vneg(axis_world) : axis_world;", 1),
+    ("weld acts only against a static parent",
+     "            if (w_b > 1e-8f) {\n                float d_lambda = (-C) / (w_b + alpha_tilde);",
+     "            if (w_b > 1e-8f && inv_mass_a == 0.0f) {\n                float d_lambda = (-C) / (w_b + alpha_tilde);", 1),
+    # read_sensors (:1799-1893)
+    ("joint position sensor reads the velocity",
+     "case 0: o[0] = e->jpos[obj]; break;", "case 0: o[0] = e->jvel[obj]; break;", 1),
 ]
 
 

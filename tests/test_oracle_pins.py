@@ -23,7 +23,13 @@ its answer; tests/test_oracle_mutants.py plants those misreadings and checks tha
                          (world.zig:736-746)
   solve_joints           point constraint on offset-COM bodies: the correction turns each
                          body about its COM (:1010-1030); slider and weld hold their
-                         build-time relative orientation (:1348-1391, world.zig:397-415)
+                         build-time relative orientation (:1348-1391, world.zig:397-415);
+                         the weld moves only the child, also under a dynamic parent; the
+                         angular limit's lower side (:1208-1212)
+  solve_contacts         the world restitution stored by the narrow phase and used by the
+                         solve (closed form of the stored impulse); the position correction
+                         keeps the pair's centre of mass (:1722-1760)
+  integrate              rotation about the world-frame angular velocity (:440-452)
 """
 import numpy as np
 import pytest
@@ -518,3 +524,89 @@ def test_geoms_of_one_body_never_pair():
     O.collide_env(w, 0)
     assert int(w.contact_counts[0]) == 2
     np.testing.assert_array_equal(w.contacts[0]["indices"][:2], [[1, 2, 0, 2], [1, 2, 1, 2]])
+
+
+# ---------------------------------------------------------------- restitution, correction split, weld
+
+FALLING_BALL = """<mujoco><option timestep="0.01"/><worldbody><geom type="plane" size="5 5 0.1"/>
+<body name="b" pos="0 0 0.09"><joint type="free"/><geom type="sphere" size="0.1" mass="2"/></body>
+</worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("e,vz", [(0.0, -2.0), (0.5, -2.0), (1.0, -2.0), (0.5, -0.3)])
+def test_contact_keeps_the_world_restitution(e, vz):
+    """The narrow phase stores the world's restitution in the contact (impulses.w) and the
+    solve uses it: a ball (m 2) driven into the plane with v_z, one iteration, no gravity,
+    stores j_n = m (-(1 + e') v_n + beta max(pen - slop, 0) / dt) with e' = e when the
+    approach is faster than 0.5 m/s, else 0; v_n = 0.999 v_z after integration and
+    pen = r - z after it. Nothing else acts on the normal (the lever is along it)."""
+    m = load_model(mjcf_string=FALLING_BALL)
+    m["restitution"] = e
+    w = O.OracleWorld(m, 1, contact_iterations=1)
+    w.gravity = [0.0, 0.0, 0.0]
+    _set(w, 1, vel=(0.0, 0.0, vz))
+    w.step(None)
+    c = w.contacts[0][0]
+    assert int(w.contact_counts[0]) == 1
+    np.testing.assert_allclose(c["impulses"][3], e)
+    vn = 0.999 * vz
+    pen = 0.1 - (0.09 + vn * 0.01)
+    e_eff = e if vn < -0.5 else 0.0
+    want = 2.0 * (-(1.0 + e_eff) * vn + 0.2 * max(pen - 0.005, 0.0) / 0.01)
+    np.testing.assert_allclose(c["impulses"][0], want, rtol=2e-5)
+
+
+def test_contact_position_correction_keeps_the_centre_of_mass():
+    """Two dynamic spheres (m 2 and 3) overlapping by 0.01 along -z: the slot's position
+    correction separates the contact points by beta (pen - slop) along the normal and splits
+    it by inverse mass, so the mass-weighted centre does not move."""
+    imi = np.zeros((3, 4), np.float32)
+    pos, vel, ang = (np.zeros((3, 4), np.float32) for _ in range(3))
+    imi[1] = [0.5, 125, 125, 125]
+    imi[2] = [1 / 3, 80, 80, 80]
+    pos[1, :3] = [0, 0, 0.1]
+    pos[2, :3] = [0, 0, 0.29]
+    c = np.zeros(1, O.CONTACT_DTYPE)
+    c["position_pen"][0] = [0, 0, 0.195, 0.01]
+    c["normal_friction"][0] = [0, 0, -1, 0.5]
+    c["indices"][0] = [1, 2, 0, 0]
+    p0 = pos.copy()
+    O.solve_contact_slot(imi, pos, vel, ang, c, 0.2, 0.005, 0.01)
+    da, db = pos[1, :3].astype(np.float64) - p0[1, :3], pos[2, :3].astype(np.float64) - p0[2, :3]
+    np.testing.assert_allclose(np.dot(da - db, [0, 0, -1]), 0.2 * (0.01 - 0.005), rtol=1e-5)
+    np.testing.assert_allclose(2.0 * da + 3.0 * db, 0.0, atol=1e-7)  # fp32 rounding of 0.29 + dz
+
+
+WELD_ON_FREE_PARENT = """<mujoco><option timestep="0.01"/><worldbody>
+<body name="a" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1" mass="1"/>
+<body name="b" pos="0.3 0 0"><geom type="sphere" size="0.1" mass="1"/></body>
+</body></worldbody></mujoco>"""
+
+
+def test_weld_moves_only_the_child():
+    """A body without a joint is welded to its parent, and the weld corrects body b only
+    (Q15), also when the parent is dynamic: the child pushed 0.2 off its anchor returns in one
+    iteration and the free parent does not move."""
+    m, w = _world(WELD_ON_FREE_PARENT, gravity=(0, 0, 0), iterations=1)
+    _set(w, 2, pos=(0.3, 0.2, 1.0))
+    w.step(None)
+    np.testing.assert_array_equal(w.positions[0, 1, :3], np.float32([0, 0, 1]))
+    np.testing.assert_allclose(w.positions[0, 2, :3], [0.3, 0, 1], atol=1e-6)
+    np.testing.assert_array_equal(w.quaternions[0, 1], np.float32([0, 0, 0, 1]))
+
+
+@pytest.mark.parametrize("iterations", [1, 3])
+def test_angular_limit_below_its_lower_bound(iterations):
+    """The angular limit's lower side (all_shaders.metal:1208-1212) with the child at -0.8 rad
+    and range (-0.5, 0.5): violation v = lower - angle > 0, and each iteration turns the child
+    by 2 atan(-v / 2) (the reference's update, which moves it away from the limit, as on the
+    upper side)."""
+    _, w = _world(HINGE_LIMIT, gravity=(0, 0, 0), iterations=iterations)
+    _set(w, 1, quat=_qaxis([0, 1, 0], -0.8))
+    w.step(None)
+    angle = -0.8
+    for _ in range(iterations):
+        angle += 2 * np.arctan(-(-0.5 - angle) / 2)
+    q = w.quaternions[0, 1].astype(np.float64)
+    got = 2 * np.arctan2(q[1], q[3])
+    assert abs(((got - angle + np.pi) % (2 * np.pi)) - np.pi) < 1e-4

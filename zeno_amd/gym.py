@@ -30,11 +30,13 @@ try:  # pragma: no cover - gymnasium is not part of this image
     import gymnasium as _gymnasium
     from gymnasium import spaces as _spaces
     from gymnasium.vector import VectorEnv as _VectorEnv
+    from gymnasium.vector.utils import batch_space as _batch_space
     HAS_GYMNASIUM = True
 except ImportError:
     _gymnasium = None
     _spaces = None
     _VectorEnv = object
+    _batch_space = None
     HAS_GYMNASIUM = False
 
 # Environment ids registered as Zeno/<name>-v0: asset file, episode limit, reward threshold.
@@ -294,13 +296,15 @@ class ZenoVectorEnv(_VectorEnv):
         self.clock = EpisodeClock(num_envs, max_episode_steps)
         self.render_mode = render_mode
         obs_dim, act_dim = self.batch.observation_dim, self.batch.action_dim
+        # The spaces are set as attributes, which both gymnasium's older VectorEnv (whose
+        # constructor takes them) and its newer one (whose constructor takes nothing) read.
+        self.num_envs = num_envs
+        self.single_observation_space = _box(-np.inf, np.inf, (obs_dim,))
+        self.single_action_space = _box(-1.0, 1.0, (act_dim,))
         if HAS_GYMNASIUM:  # pragma: no cover
-            super().__init__(num_envs=num_envs, observation_space=_box(-np.inf, np.inf, (obs_dim,)),
-                             action_space=_box(-1.0, 1.0, (act_dim,)))
+            self.observation_space = _batch_space(self.single_observation_space, num_envs)
+            self.action_space = _batch_space(self.single_action_space, num_envs)
         else:
-            self.num_envs = num_envs
-            self.single_observation_space = Box(-np.inf, np.inf, (obs_dim,))
-            self.single_action_space = Box(-1.0, 1.0, (act_dim,))
             self.observation_space = Box(-np.inf, np.inf, (num_envs, obs_dim))
             self.action_space = Box(-1.0, 1.0, (num_envs, act_dim))
         self.closed = False
