@@ -230,6 +230,115 @@ MUTANTS = [
     # read_sensors (:1799-1893)
     ("joint position sensor reads the velocity",
      "case 0: o[0] = e->jpos[obj]; break;", "case 0: o[0] = e->jvel[obj]; break;", 1),
+    # extended narrow phase: detectCollision and its pairs (narrow_phase.zig:28-512, 786-925)
+    ("sphere-sphere: point ra + pen/2",
+     "v3 point = vadd(pa, vscale(n, ra - pen * 0.5f));\n    return np_emit",
+     "v3 point = vadd(pa, vscale(n, ra + pen * 0.5f));\n    return np_emit", 1),
+    ("sphere-sphere: local_b on the far side",
+     "float pen = min_dist - dist;\n    v3 point = vadd(pa, vscale(n, ra - pen * 0.5f));\n    return np_emit(out, point, n, pen, vscale(n, ra), vscale(n, -rb));",
+     "float pen = min_dist - dist;\n    v3 point = vadd(pa, vscale(n, ra - pen * 0.5f));\n    return np_emit(out, point, n, pen, vscale(n, ra), vscale(n, rb));", 1),
+    ("sphere-capsule: point offset by the sphere radius",
+     "v3 point = vadd(closest, vscale(n, cr - pen * 0.5f));",
+     "v3 point = vadd(closest, vscale(n, sr - pen * 0.5f));", 1),
+    ("sphere-capsule: local_a toward the capsule",
+     "return np_emit(out, point, n, pen, vscale(n, sr), vscale(n, -cr));",
+     "return np_emit(out, point, n, pen, vscale(n, -sr), vscale(n, -cr));", 1),
+    ("sphere-plane: plane offset dropped",
+     "float signed_dist = vdot(vsub(sp, pp), n) - pl->size[0];",
+     "float signed_dist = vdot(vsub(sp, pp), n);", 1),
+    ("sphere-plane: point on the far side",
+     "v3 point = vsub(sp, vscale(n, signed_dist + pen * 0.5f));",
+     "v3 point = vsub(sp, vscale(n, signed_dist - pen * 0.5f));", 1),
+    ("sphere-plane: local_a sign",
+     "return np_emit(out, point, n, pen, vscale(n, -sr), V(0.0f, 0.0f, 0.0f));",
+     "return np_emit(out, point, n, pen, vscale(n, sr), V(0.0f, 0.0f, 0.0f));", 1),
+    ("plane point without the geom offset",
+     "v3 pp = np_point(pl, ld3(pl->local_pos));",
+     "v3 pp = np_point(pl, V(0.0f, 0.0f, 0.0f));", 3),
+    ("geom centre without the geom offset",
+     "v3 pa = np_point(a, ld3(a->local_pos));\n    v3 pb = np_point(b, ld3(b->local_pos));",
+     "v3 pa = V(a->position[0], a->position[1], a->position[2]);\n    v3 pb = V(b->position[0], b->position[1], b->position[2]);", 1),
+    ("box face normal: positive face sign",
+     "if (dpos > maxd) { maxd = dpos; nrm[0] = nrm[1] = nrm[2] = 0.0f; nrm[i] = 1.0f; }",
+     "if (dpos > maxd) { maxd = dpos; nrm[0] = nrm[1] = nrm[2] = 0.0f; nrm[i] = -1.0f; }", 1),
+    ("box face normal: nearest face",
+     "if (dpos > maxd) { maxd = dpos;",
+     "if (dpos < maxd || maxd == -INFINITY) { maxd = dpos;", 1),
+    ("sphere-box: point inside the box",
+     "v3 point = vadd(wc, vscale(n, pen * 0.5f));",
+     "v3 point = vsub(wc, vscale(n, pen * 0.5f));", 1),
+    ("sphere-box: local_b without the geom offset",
+     "vsub(cl, ld3(box->local_pos))",
+     "cl", 1),
+    ("sphere-box: sphere rotated by q, not its inverse",
+     "v3 r = np_rot(sp, iq);",
+     "v3 r = np_rot(sp, q);", 1),
+    ("segment point: no clamp",
+     "float t = np_clamp(vdot(vsub(p, s), seg) / len_sq, 0.0f, 1.0f);",
+     "float t = vdot(vsub(p, s), seg) / len_sq;", 1),
+    ("segments: t>1 branch sign",
+     "s = np_clamp((b - c) / a, 0.0f, 1.0f);",
+     "s = np_clamp((b + c) / a, 0.0f, 1.0f);", 1),
+    ("segments: t sign of f",
+     "t = (b * s + f) / e;",
+     "t = (b * s - f) / e;", 1),
+    ("segments: degenerate a sign",
+     "t = np_clamp(f / e, 0.0f, 1.0f);",
+     "t = np_clamp(-f / e, 0.0f, 1.0f);", 1),
+    ("segments: degenerate b sign",
+     "        if (e < ZO_NP_EPS) {\n            s = np_clamp(-c / a, 0.0f, 1.0f);",
+     "        if (e < ZO_NP_EPS) {\n            s = np_clamp(c / a, 0.0f, 1.0f);", 1),
+    ("segments: t<0 branch keeps s",
+     "                t = 0.0f;\n                s = np_clamp(-c / a, 0.0f, 1.0f);",
+     "                t = 0.0f;", 1),
+    ("segments: parallel s = 1",
+     "if (denom != 0.0f) s = np_clamp((b * f - c * e) / denom, 0.0f, 1.0f);",
+     "s = denom != 0.0f ? np_clamp((b * f - c * e) / denom, 0.0f, 1.0f) : 1.0f;", 1),
+    ("capsule-capsule: point b on the far side",
+     "v3 wb = vsub(qb, vscale(n, rb));",
+     "v3 wb = vadd(qb, vscale(n, rb));", 1),
+    ("capsule-plane: point below by dist/2 - radius",
+     "v3 point = vsub(deepest, vscale(n, dist * 0.5f + radius));",
+     "v3 point = vsub(deepest, vscale(n, dist * 0.5f - radius));", 1),
+    ("capsule-plane: local_a sign",
+     "return np_emit(out, point, n, -dist, vscale(n, -radius), V(0.0f, 0.0f, 0.0f));",
+     "return np_emit(out, point, n, -dist, vscale(n, radius), V(0.0f, 0.0f, 0.0f));", 1),
+    ("capsule-plane: shallower endpoint",
+     "v3 deepest = d1 < d2 ? p1 : p2;\n    float dist = np_min(d1, d2);",
+     "v3 deepest = d1 < d2 ? p2 : p1;\n    float dist = np_min(d1, d2);", 1),
+    ("box-plane: local_a in world frame",
+     "return np_emit(out, dw, n, -min_dist, dc,",
+     "return np_emit(out, dw, n, -min_dist, dw,", 1),
+    ("box-plane: point at the midpoint",
+     "return np_emit(out, dw, n, -min_dist, dc,",
+     "return np_emit(out, vsub(dw, vscale(n, min_dist * 0.5f)), n, -min_dist, dc,", 1),
+    ("box-plane: plane offset applied",
+     "float dist = vdot(vsub(wc, pp), n);",
+     "float dist = vdot(vsub(wc, pp), n) - pl->size[0];", 1),
+    ("box-box: normal toward a",
+     "if (vdot(best, d) < 0.0f) best",
+     "if (vdot(best, d) > 0.0f) best", 1),
+    ("box-box: edge axes skipped",
+     "if (len < ZO_NP_EPS) continue;",
+     "continue;", 1),
+    ("box-box: point at a's centre",
+     "v3 point = vadd(pa, vscale(d, 0.5f));",
+     "v3 point = pa;", 1),
+    ("box-box: projection with b's half-extents for a",
+     "float proj_a = ha[0] * fabsf(vdot(axis, xa[0]))",
+     "float proj_a = hb[0] * fabsf(vdot(axis, xa[0]))", 1),
+    ("flip: locals not swapped",
+     "float t = r->local_a[i]; r->local_a[i] = r->local_b[i]; r->local_b[i] = t;",
+     "", 1),
+    ("dispatch: box-sphere not flipped",
+     "hit = np_sphere_box(pb, b->size[0], a, out); if (hit) np_flip(out);",
+     "hit = np_sphere_box(pb, b->size[0], a, out);", 1),
+    ("dispatch: plane-capsule not flipped",
+     "hit = np_capsule_plane(pb, b, a, out); if (hit) np_flip(out);",
+     "hit = np_capsule_plane(pb, b, a, out);", 1),
+    ("rotation: conjugate quaternion",
+     "v3 qv = V(q[0], q[1], q[2]);\n    v3 uv = vcross(qv, v);",
+     "v3 qv = V(-q[0], -q[1], -q[2]);\n    v3 uv = vcross(qv, v);", 1),
 ]
 
 
@@ -257,7 +366,7 @@ def _build_and_run(src_text: str, workdir: Path) -> subprocess.CompletedProcess:
 
 @pytest.fixture(scope="module")
 def results():
-    """Runs the unmutated copy and every mutant (4 child processes at a time)."""
+    """Runs the unmutated copy and every mutant (up to 6 child processes at a time)."""
     if shutil.which("gcc") is None:
         pytest.skip("gcc is required")
     source = SRC.read_text()
@@ -266,7 +375,7 @@ def results():
         assert source.count(orig) == n, f"mutation site for '{name}' found {source.count(orig)} times, not {n}"
         jobs[name] = source.replace(orig, mut)
     with tempfile.TemporaryDirectory() as tmp:
-        with ThreadPoolExecutor(max_workers=4) as pool:
+        with ThreadPoolExecutor(max_workers=max(2, min(6, (os.cpu_count() or 4) - 2))) as pool:
             futs = {k: pool.submit(_build_and_run, v, Path(tmp) / f"m{i}") for i, (k, v) in enumerate(jobs.items())}
             yield {k: f.result() for k, f in futs.items()}
 
