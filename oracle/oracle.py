@@ -119,7 +119,10 @@ class OracleWorld:
         self.lib = load()
         self.model = model
         E, B = num_envs, model["num_bodies"]
-        J, A, N = model["num_joints"], model["num_actuators"], model["num_constraints"]
+        # The constraint templates, colours and colour ranges come from the oracle's own builder
+        # (zo_build_templates), not from the product's model records.
+        tmpl, ranges, self.num_colors = build_templates(model)
+        J, A, N = model["num_joints"], model["num_actuators"], len(tmpl)
         Jp, Op, M = max(J, 1), max(model["obs_dim"], 1), max_contacts_per_env
         self.E, self.B, self.J, self.A, self.N, self.M = E, B, J, A, N, M
         self.timestep = float(timestep if timestep > 0 else model["timestep"])
@@ -144,20 +147,19 @@ class OracleWorld:
         self.prev_contact_counts = np.zeros(E, np.uint32)
         self.cell_ids = np.zeros((E, max(model["num_geoms"], 1)), np.uint32)
         self.extended_contacts = False
-        tmpl = model["constraints"]
         self.constraints = np.ascontiguousarray(np.broadcast_to(tmpl, (E, N)), CONSTRAINT_DTYPE).copy()
         if N:
             self.constraints["indices"][:, :, 2] = np.arange(E, dtype=np.uint32)[:, None]
         self._keep = {k: np.ascontiguousarray(model[k]) for k in
                       ("bodies", "joints", "geoms", "actuators", "sensors")}
-        self._keep["color_ranges"] = np.ascontiguousarray(model["color_ranges"], dtype=np.uint32).reshape(-1)
+        self._keep["color_ranges"] = np.ascontiguousarray(ranges, dtype=np.uint32).reshape(-1)
 
     def _model_struct(self) -> ZoModel:
         m = self.model
         zm = ZoModel()
         zm.num_envs, zm.num_bodies, zm.num_joints = self.E, self.B, self.J
         zm.num_geoms, zm.num_actuators, zm.num_sensors = m["num_geoms"], self.A, m["num_sensors"]
-        zm.obs_dim, zm.num_constraints, zm.num_colors = m["obs_dim"], self.N, m["num_colors"]
+        zm.obs_dim, zm.num_constraints, zm.num_colors = m["obs_dim"], self.N, self.num_colors
         zm.max_contacts, zm.contact_iterations, zm.config_substeps = self.M, self.contact_iterations, self.substeps
         zm.timestep = self.timestep
         for i in range(3):

@@ -132,6 +132,7 @@ def test_free_joint_has_no_constraints_and_implicit_fixed_joint():
 
 @pytest.mark.parametrize("jtype,rng,expect", [
     ("hinge", "", [2, 3]), ("hinge", ' range="-1 1"', [2, 3, 4]), ("hinge", ' range="1 -1"', [2, 3]),
+    ("hinge", ' range="0.3 0.3"', [2, 3]), ("slide", ' range="0.3 0.3"', [10]), ("ball", ' range="0.5 0.5"', [2]),
     ("slide", "", [10]), ("slide", ' range="-1 1"', [10, 5]),
     ("ball", "", [2]), ("ball", ' range="0 0.5"', [2, 4]), ("free", "", []),
 ])
@@ -144,7 +145,7 @@ def test_decomposition(jtype, rng, expect):
     m = load_model(mjcf_string=xml)
     t = m["constraints"]
     assert sorted(ctype(t).tolist()) == sorted(expect)
-    if jtype == "ball" and rng:
+    if jtype == "ball" and 4 in expect:
         lim = t[ctype(t) == 4]
         np.testing.assert_allclose(lim["limits"][0, :2], [-0.5, 0.5])
 

@@ -19,8 +19,11 @@ How each oracle function is pinned:
                             position correction per iteration, velocity overwrite)
   k_apply_actions           reference actuator KATs (test_physics_integration.zig:517-629)
   k_read_sensors            Ant obs[0:13] reads the world body (frame sensors ignore objname)
-  zo_build_templates        agrees with the product's independently written builder, and with
-                            fixtures C1-C4
+  zo_build_templates        fixtures C1-C4 directly; each joint type's template fields from
+                            float64 rotations; limits only for lower < upper; the world body
+                            counted in the colouring; and agreement with the product's
+                            independently written builder (OracleWorld steps with the oracle's
+                            own templates)
 """
 import json
 from pathlib import Path
@@ -356,6 +359,133 @@ def test_template_builders_agree_on_assets(name):
     t, ranges, ncol = O.build_templates(m)
     assert t.tobytes() == m["constraints"].tobytes()
     np.testing.assert_array_equal(ranges, m["color_ranges"])
+
+
+@pytest.mark.parametrize("name", ["pendulum", "cartpole", "ant", "humanoid"])
+def test_oracle_templates_match_fixtures(name):
+    """The oracle's own builder against fixtures C1-C4 (constraint types, bodies, colours,
+    the stable colour sort and the colour ranges), without the product's builder."""
+    m = load_model(str(ASSETS / f"{name}.xml"))
+    t, ranges, ncol = O.build_templates(m)
+    g = GOLD[name]
+    if "templates_joint_order" in g:
+        expect = sorted(g["templates_joint_order"], key=lambda r: r[3])
+        np.testing.assert_array_equal(ranges, g["color_ranges"])
+    else:
+        pre = []
+        for a, b, base in g["hinge_triples"]:
+            pre += [[2, a, b, base], [3, a, b, base + 1], [4, a, b, base + 2]]
+        expect = sorted(pre, key=lambda r: r[3])
+        np.testing.assert_array_equal(ranges[:, 1], g["color_sizes"])
+        np.testing.assert_array_equal(ranges[:, 0], np.cumsum([0] + g["color_sizes"][:-1]))
+    got = [[int(r[3] & 0xFF), int(r[0]), int(r[1]), int((r[3] >> 8) & 0xFF)] for r in t["indices"]]
+    assert got == expect
+    assert ncol == g["counts"]["num_colors"]
+
+
+def _rot64(q):
+    x, y, z, w = (float(v) for v in q)
+    return np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - z * w), 2 * (x * z + y * w)],
+                     [2 * (x * y + z * w), 1 - 2 * (x * x + z * z), 2 * (y * z - x * w)],
+                     [2 * (x * z - y * w), 2 * (y * z + x * w), 1 - 2 * (x * x + y * y)]])
+
+
+def _qmul64(a, b):
+    ax, ay, az, aw = (float(v) for v in a)
+    bx, by, bz, bw = (float(v) for v in b)
+    return np.array([aw * bx + ax * bw + ay * bz - az * by, aw * by - ax * bz + ay * bw + az * bx,
+                     aw * bz + ax * by - ay * bx + az * bw, aw * bw - ax * bx - ay * by - az * bz])
+
+
+TEMPLATE_SCENE = """<mujoco><worldbody>
+<body name="p" pos="0.2 -0.1 1" quat="0.9 0.3 -0.2 0.25"><joint type="free"/><geom type="sphere" size="0.1"/>
+  <body name="c" pos="0.3 0.1 -0.2" quat="0.7 -0.4 0.5 0.3">
+    <joint type="{kind}" pos="0.05 -0.02 0.1" axis="0.3 -0.5 0.8"{extra}/>
+    <geom type="sphere" size="0.1"/></body>
+</body></worldbody></mujoco>"""
+
+
+@pytest.mark.parametrize("kind,extra,joint_type", [
+    ("hinge", ' range="-0.7 0.4" damping="0.3"', 1), ("slide", ' range="-0.2 0.5" damping="0.6"', 2),
+    ("ball", ' range="0 0.6"', 3), ("hinge", "", 5), ("hinge", ' range="-0.7 0.4"', 0)])
+def test_oracle_template_fields_closed_form(kind, extra, joint_type):
+    """Each joint type's templates field by field (joint.zig:202-350, world.zig:311-501), from
+    float64 rotations of the bodies' initial quaternions: weld anchors and target conj(q_p) q_c;
+    revolute point anchors, hinge axis in the parent frame and, in anchor_b, the same axis in the
+    child frame with the damping in w, angular limit (lower, upper); prismatic slider anchors,
+    damping, axis and target, linear limit on the child anchor; ball cone limit (-upper, upper);
+    universal hinges about the axis and about (0, 1, 0). Joint types 0 (fixed) and 5 (universal)
+    are set on the revolute's record: MJCF never makes them for a body with a joint."""
+    m = load_model(mjcf_string=TEMPLATE_SCENE.format(kind=kind, extra=extra))
+    j = int(np.flatnonzero(m["joints"]["params"][:, 0] != 4)[0])
+    if joint_type in (0, 5):
+        m["joints"]["params"][j, 0] = joint_type
+    jd = m["joints"][j]
+    a, b = int(jd["params"][1]), int(jd["params"][2])
+    qa, qb = m["bodies"]["quaternion"][a], m["bodies"]["quaternion"][b]
+    ap, ac, ax = (np.asarray(jd[k][:3], np.float64) for k in ("anchor_parent", "anchor_child", "axis"))
+    lower, upper, damping = float(jd["params"][3]), float(jd["params2"][0]), float(jd["params2"][1])
+    rel = _qmul64(np.r_[-qa[:3], qa[3]], qb)
+    to_child = lambda v: _rot64(qb).T @ (_rot64(qa) @ v)
+    t, _, _ = O.build_templates(m)
+    rows = [r for r in t if (int(r["indices"][0]), int(r["indices"][1])) == (a, b)]
+    types = [int(r["indices"][3] & 0xFF) for r in rows]
+    by = {ty: [r for r in rows if int(r["indices"][3] & 0xFF) == ty] for ty in set(types)}
+    close = lambda x, y: np.testing.assert_allclose(np.asarray(x, np.float64), y, atol=2e-6)
+    if joint_type == 0:
+        assert types == [7]
+        close(by[7][0]["anchor_a"][:3], ap); close(by[7][0]["anchor_b"][:3], ac); close(by[7][0]["axis_target"], rel)
+    elif joint_type == 1:
+        assert types == [2, 3, 4]
+        close(by[2][0]["anchor_a"][:3], ap); close(by[2][0]["anchor_b"][:3], ac)
+        close(by[3][0]["anchor_a"][:3], ax); close(by[3][0]["anchor_b"][:3], to_child(ax))
+        assert by[3][0]["anchor_b"][3] == np.float32(damping) and damping > 0
+        close(by[4][0]["anchor_a"][:3], ax); close(by[4][0]["limits"][:2], [lower, upper])
+    elif joint_type == 2:
+        assert types == [10, 5]
+        r = by[10][0]
+        close(r["anchor_a"][:3], ap); close(r["anchor_b"][:3], ac); close(r["axis_target"][:3], ax)
+        assert r["anchor_b"][3] == np.float32(damping) and damping > 0
+        close(r["limits"], rel)
+        close(by[5][0]["anchor_a"][:3], ax); close(by[5][0]["anchor_b"][:3], ac)
+        close(by[5][0]["limits"][:2], [lower, upper])
+    elif joint_type == 3:
+        assert types == [2, 4]
+        close(by[4][0]["anchor_a"][:3], ax); close(by[4][0]["limits"][:2], [-upper, upper])
+    else:
+        assert types == [2, 3, 3]
+        close(by[3][0]["anchor_a"][:3], ax); close(by[3][0]["anchor_b"][:3], to_child(ax))
+        y = np.array([0.0, 1.0, 0.0])
+        close(by[3][1]["anchor_a"][:3], y); close(by[3][1]["anchor_b"][:3], to_child(y))
+
+
+@pytest.mark.parametrize("jtype,rng,expect", [
+    ("hinge", "", [2, 3]), ("hinge", ' range="-1 1"', [2, 3, 4]), ("hinge", ' range="1 -1"', [2, 3]),
+    ("hinge", ' range="0.3 0.3"', [2, 3]), ("slide", ' range="0.3 0.3"', [10]), ("ball", ' range="0.5 0.5"', [2]),
+    ("slide", "", [10]), ("slide", ' range="-1 1"', [10, 5]), ("ball", "", [2]), ("ball", ' range="0 0.5"', [2, 4]),
+    ("free", "", [])])
+def test_oracle_decomposition_limits_need_lower_below_upper(jtype, rng, expect):
+    """The oracle's builder adds a limit only for a limited joint with lower < upper
+    (Joint.hasLimits, joint.zig:70-72); equal bounds give none."""
+    xml = f"""<mujoco><worldbody><body name="a" pos="0 0 1"><joint type="{jtype}" axis="0 1 0"{rng}/>
+    <geom type="sphere" size="0.1"/></body></worldbody></mujoco>"""
+    t, _, _ = O.build_templates(load_model(mjcf_string=xml))
+    assert [int(x) & 0xFF for x in t["indices"][:, 3]] == expect
+
+
+def test_oracle_colouring_counts_the_world_body():
+    """Constraints on the world body share it (xpbd.zig:551-575 lists every body below
+    num_bodies, the world included): two bodies hinged to the world take colours 0, 1 (first
+    point and hinge), then 2, 3."""
+    xml = """<mujoco><worldbody>
+    <body name="a" pos="0 0 1"><joint type="hinge" axis="0 1 0"/><geom type="sphere" size="0.1"/></body>
+    <body name="b" pos="1 0 1"><joint type="hinge" axis="0 1 0"/><geom type="sphere" size="0.1"/></body>
+    </worldbody></mujoco>"""
+    t, ranges, ncol = O.build_templates(load_model(mjcf_string=xml))
+    got = [[int(r[3] & 0xFF), int(r[0]), int(r[1]), int((r[3] >> 8) & 0xFF)] for r in t["indices"]]
+    assert got == [[2, 0, 1, 0], [3, 0, 1, 1], [2, 0, 2, 2], [3, 0, 2, 3]]
+    assert ncol == 4
+    np.testing.assert_array_equal(ranges, [[0, 1], [1, 1], [2, 1], [3, 1]])
 
 
 # ---- joint solver closed forms (one body on the world or two free bodies, no gravity) ----

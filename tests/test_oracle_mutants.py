@@ -22,6 +22,11 @@ SRC = ROOT / "oracle" / "zeno_oracle.c"
 PINS = ["tests/test_oracle.py", "tests/test_model.py", "tests/test_hash.py", "tests/test_contact_solve.py",
         "tests/test_oracle_pins.py", "tests/test_narrow_ext.py", "tests/test_ext_contacts.py"]
 
+# The two builders of constraint templates (the product's and the oracle's) are compared with
+# each other outside this check; here they are left out, so that a mutant of the oracle's
+# builder must be caught by a pin of what the templates hold.
+DESELECT = ["--deselect", "tests/test_oracle.py::test_template_builders_agree"]
+
 # (name, original text, mutated text, occurrences); the original must occur exactly that many
 # times in the source, and every occurrence is replaced. Leading whitespace picks one site
 # where the same line appears at two depths.
@@ -339,6 +344,70 @@ MUTANTS = [
     ("rotation: conjugate quaternion",
      "v3 qv = V(q[0], q[1], q[2]);\n    v3 uv = vcross(qv, v);",
      "v3 qv = V(-q[0], -q[1], -q[2]);\n    v3 uv = vcross(qv, v);", 1),
+    # constraint templates and colouring (joint.zig:202-350, world.zig:311-501, xpbd.zig:533-640)
+    ("weld target conj(q_c) q_p",
+     "tmpl(c, a, b, 7);\n                st3(c->anchor_a, ap); st3(c->anchor_b, ac);\n                st4(c->axis_target, qmul(qconj(qa), qb));",
+     "tmpl(c, a, b, 7);\n                st3(c->anchor_a, ap); st3(c->anchor_b, ac);\n                st4(c->axis_target, qmul(qconj(qb), qa));", 1),
+    ("weld anchors swapped",
+     "tmpl(c, a, b, 7);\n                st3(c->anchor_a, ap); st3(c->anchor_b, ac);",
+     "tmpl(c, a, b, 7);\n                st3(c->anchor_a, ac); st3(c->anchor_b, ap);", 1),
+    ("revolute point anchors swapped",
+     "c = &out[n++]; tmpl(c, a, b, 2);\n                st3(c->anchor_a, ap); st3(c->anchor_b, ac);\n                c = &out[n++]; tmpl(c, a, b, 3);\n                v3 axb",
+     "c = &out[n++]; tmpl(c, a, b, 2);\n                st3(c->anchor_a, ac); st3(c->anchor_b, ap);\n                c = &out[n++]; tmpl(c, a, b, 3);\n                v3 axb", 1),
+    ("hinge child axis without the parent rotation",
+     "v3 axb = host_rot(host_rot(ax, qa), qconj(qb));",
+     "v3 axb = host_rot(ax, qconj(qb));", 1),
+    ("hinge child axis left in the world frame",
+     "v3 axb = host_rot(host_rot(ax, qa), qconj(qb));",
+     "v3 axb = host_rot(ax, qa);", 1),
+    ("hinge damping not stored",
+     "st3(c->anchor_a, ax); st3(c->anchor_b, axb); c->anchor_b[3] = damping;",
+     "st3(c->anchor_a, ax); st3(c->anchor_b, axb);", 1),
+    ("angular limit axis in the child frame",
+     "c = &out[n++]; tmpl(c, a, b, 4);\n                    st3(c->anchor_a, ax); c->limits[0] = lower;",
+     "c = &out[n++]; tmpl(c, a, b, 4);\n                    st3(c->anchor_a, axb); c->limits[0] = lower;", 1),
+    ("angular limit bounds swapped",
+     "st3(c->anchor_a, ax); c->limits[0] = lower; c->limits[1] = upper;\n                }\n                break;\n            }\n            case 2:",
+     "st3(c->anchor_a, ax); c->limits[0] = upper; c->limits[1] = lower;\n                }\n                break;\n            }\n            case 2:", 1),
+    ("limit when lower == upper",
+     "int has_limits = limited[j] && lower < upper;",
+     "int has_limits = limited[j] && lower <= upper;", 1),
+    ("slider target conj(q_c) q_p",
+     "st4(c->limits, qmul(qconj(qa), qb));",
+     "st4(c->limits, qmul(qconj(qb), qa));", 1),
+    ("slider damping not stored",
+     "st3(c->anchor_a, ap); st3(c->anchor_b, ac); c->anchor_b[3] = damping;",
+     "st3(c->anchor_a, ap); st3(c->anchor_b, ac);", 1),
+    ("slider axis rotated to the world",
+     "st3(c->axis_target, ax);",
+     "st3(c->axis_target, host_rot(ax, qa));", 1),
+    ("linear limit on the parent anchor",
+     "st3(c->anchor_a, ax); st3(c->anchor_b, ac);\n                    c->limits[0] = lower;",
+     "st3(c->anchor_a, ax); st3(c->anchor_b, ap);\n                    c->limits[0] = lower;", 1),
+    ("ball cone limit (lower, upper)",
+     "c->limits[0] = -upper; c->limits[1] = upper;",
+     "c->limits[0] = lower; c->limits[1] = upper;", 1),
+    ("universal second axis x",
+     "v3 ax2 = V(0, 1, 0);",
+     "v3 ax2 = V(1, 0, 0);", 1),
+    ("universal second hinge in the parent frame",
+     "st3(c->anchor_a, ax2); st3(c->anchor_b, host_rot(host_rot(ax2, qa), qconj(qb)));",
+     "st3(c->anchor_a, ax2); st3(c->anchor_b, ax2);", 1),
+    ("colouring ignores the world body",
+     "if (a < num_bodies && (ka == a || kb == a)) shares = 1;",
+     "if (a > 0 && a < num_bodies && (ka == a || kb == a)) shares = 1;", 1),
+    ("colour sort descending",
+     "while (j >= 0 && ((out[j].indices[3] >> 8) & 0xFF) > kc)",
+     "while (j >= 0 && ((out[j].indices[3] >> 8) & 0xFF) < kc)", 1),
+    ("colour sort unstable",
+     "while (j >= 0 && ((out[j].indices[3] >> 8) & 0xFF) > kc)",
+     "while (j >= 0 && ((out[j].indices[3] >> 8) & 0xFF) >= kc)", 1),
+    ("colour takes the largest used + 1",
+     "while (col < 255 && used[col]) ++col;",
+     "for (uint32_t u = 0; u < 255; ++u) if (used[u]) col = u + 1;", 1),
+    ("host rotation by the conjugate",
+     "float t0 = 2.0f * (q.y * v.z - q.z * v.y);\n    float t1 = 2.0f * (q.z * v.x - q.x * v.z);\n    float t2 = 2.0f * (q.x * v.y - q.y * v.x);\n    return V(v.x + q.w * t0",
+     "float t0 = 2.0f * (q.y * v.z - q.z * v.y);\n    float t1 = 2.0f * (q.z * v.x - q.x * v.z);\n    float t2 = 2.0f * (q.x * v.y - q.y * v.x);\n    return V(v.x - q.w * t0", 1),
 ]
 
 
@@ -353,7 +422,7 @@ def _build(src_text: str, out: Path) -> None:
 
 def _run_pins(lib: Path) -> subprocess.CompletedProcess:
     env = dict(os.environ, ZENO_ORACLE_LIB=str(lib), PYTHONPATH=str(ROOT), OMP_NUM_THREADS="1")
-    return subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", *PINS],
+    return subprocess.run([sys.executable, "-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", *PINS, *DESELECT],
                           cwd=str(ROOT), env=env, capture_output=True, text=True, timeout=600)
 
 
