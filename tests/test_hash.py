@@ -9,6 +9,10 @@ it on above 512 geoms) with checks that do not restate its loops:
   vs O(G^2)       with every geom inside the grid and radius sums + 0.1 below one cell, the
                   non-plane pairs equal those of the O(G^2) broad phase
   plane reach     a plane pairs only with geoms in the 27 cells around its own cell
+  filters         geoms sharing a body, contype/conaffinity masks and geom offsets, against
+                  the same set definition
+  threshold       the step takes the hash above 512 geoms only
+  overflow        the count runs past the list's capacity; the first entries are kept
 """
 import numpy as np
 import pytest
@@ -18,9 +22,11 @@ from zeno_amd.model import load_model
 from zeno_amd.scenes import PILES, pile_initial_state, pile_mjcf
 
 
-def _pile(name="pile_hash", num_envs=1, max_contacts=64, seed=0):
+def _pile(name="pile_hash", num_envs=1, max_contacts=64, seed=0, edit=None):
     nb, xy = PILES[name]
     m = load_model(mjcf_string=pile_mjcf(nb, seed=seed, xy=xy))
+    if edit is not None:
+        edit(m)
     o = O.OracleWorld(m, num_envs, max_contacts_per_env=max_contacts)
     o.reset_to_state(*pile_initial_state(m, num_envs, seed + 1, xy=xy))
     return m, o
@@ -118,3 +124,70 @@ def test_plane_reaches_only_neighbouring_cells():
     _, con, n = O.broad_phase_hash(o, 0)
     planes = [tuple(int(v) for v in r) for r in con["indices"][:n] if r[2] == 0]
     assert planes == [(0, 1, 0, 1)]
+
+
+@pytest.mark.parametrize("nb,hashed", [(511, False), (512, True)])
+def test_hash_only_above_512_geoms(nb, hashed):
+    """World.stepOnce takes the spatial hash only when num_geoms > 512 (world.zig:534). With
+    every body far from the plane's cell and from each other, the list broad phase still pairs
+    the plane with each of them (planes skip the distance test), the hash with none."""
+    m = load_model(mjcf_string=pile_mjcf(nb, seed=0))
+    assert m["num_geoms"] == nb + 1
+    o = O.OracleWorld(m, 1, max_contacts_per_env=1024)
+    o.gravity = [0.0, 0.0, 0.0]
+    k = np.arange(nb)
+    o.positions[0, 1:, 0] = 30.0 + 1.5 * (k % 8)
+    o.positions[0, 1:, 1] = 30.0 + 1.5 * ((k // 8) % 8)
+    o.positions[0, 1:, 2] = 40.0 + 1.5 * (k // 64)
+    o.velocities[:] = 0.0
+    o.angular_velocities[:] = 0.0
+    o.step(None)
+    assert int(o.contact_counts[0]) == (0 if hashed else nb)
+
+
+def test_geom_offset_moves_the_cell():
+    """A geom's cell is that of its body position plus its offset (all_shaders.metal:574-580)."""
+    def edit(m):
+        m["geoms"]["pos_size0"][1, :3] = (0.7, -0.2, 1.6)
+    m, o = _pile(edit=edit)
+    o.positions[0, 1, :3] = (0.5, 0.5, 0.5)
+    ids, _, _ = O.broad_phase_hash(o, 0)
+    assert ids[1] == 1 + 0 * 64 + 2 * 4096
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_pairs_with_shared_bodies_masks_and_offsets(seed):
+    """Geoms moved onto a neighbour's body, given offsets and random contype/conaffinity
+    masks: the pairs still follow the set definition (same-body pairs dropped, a pair kept
+    when either geom's contype meets the other's conaffinity, positions with offsets)."""
+    rng = np.random.default_rng(100 + seed)
+
+    def edit(m):
+        tb, ps = m["geoms"]["type_body"], m["geoms"]["pos_size0"]
+        G = len(tb)
+        share = np.arange(2, G, 3)
+        tb[share, 1] = tb[share - 1, 1]
+        ps[1:, :3] = rng.uniform(-0.3, 0.3, (G - 1, 3))
+        tb[1:, 2] = rng.integers(0, 4, G - 1)
+        tb[1:, 3] = rng.integers(0, 4, G - 1)
+    m, o = _pile(max_contacts=60000, seed=seed, edit=edit)
+    _, con, n = O.broad_phase_hash(o, 0)
+    want = _expected_pairs(m, o.positions[0])
+    got = [tuple(int(v) for v in r) for r in con["indices"][:n]]
+    assert got == want
+    tb = m["geoms"]["type_body"]
+    same = [(g, x) for g in range(len(tb)) for x in range(g + 1, min(g + 3, len(tb))) if tb[g, 1] == tb[x, 1]]
+    assert len(same) > 100 and not any((p[2], p[3]) in set(same) for p in got)
+    masked = sum(1 for p in _expected_pairs(m, o.positions[0]) if (tb[p[2], 3] & tb[p[3], 2]) == 0)
+    assert masked > 0  # pairs kept through the other direction of the mask rule
+
+
+def test_count_runs_past_the_list_capacity():
+    """The counter takes every pair (atomic add before the capacity check, all_shaders.metal:
+    692-698); only the first M are written."""
+    _, big = _pile(max_contacts=60000)
+    _, full, n_full = O.broad_phase_hash(big, 0)
+    _, small = _pile(max_contacts=16)
+    _, con, n = O.broad_phase_hash(small, 0)
+    assert n == n_full > 16
+    np.testing.assert_array_equal(con["indices"][:16], full["indices"][:16])

@@ -408,6 +408,49 @@ MUTANTS = [
     ("host rotation by the conjugate",
      "float t0 = 2.0f * (q.y * v.z - q.z * v.y);\n    float t1 = 2.0f * (q.z * v.x - q.x * v.z);\n    float t2 = 2.0f * (q.x * v.y - q.y * v.x);\n    return V(v.x + q.w * t0",
      "float t0 = 2.0f * (q.y * v.z - q.z * v.y);\n    float t1 = 2.0f * (q.z * v.x - q.x * v.z);\n    float t2 = 2.0f * (q.x * v.y - q.y * v.x);\n    return V(v.x - q.w * t0", 1),
+    # spatial-hash broad phase (all_shaders.metal:556-703, world.zig:534)
+    ("hash threshold >= 512",
+     "if (e->m->num_geoms > ZO_HASH_MIN_GEOMS)",
+     "if (e->m->num_geoms >= ZO_HASH_MIN_GEOMS)", 1),
+    ("hash cell by ceil",
+     "float f = floorf(p * 1.0f);",
+     "float f = ceilf(p * 1.0f);", 1),
+    ("hash NaN in the last cell",
+     "if (!(f >= 0.0f)) return 0u;",
+     "if (f != f) return ZO_HASH_DIM - 1u;\n    if (!(f >= 0.0f)) return 0u;", 1),
+    ("hash huge coordinates past the last cell",
+     "if (f >= (float)(ZO_HASH_DIM - 1u)) return ZO_HASH_DIM - 1u;",
+     "if (f >= (float)ZO_HASH_DIM) return ZO_HASH_DIM;", 1),
+    ("hash id z-major",
+     "uint32_t id = cx[3 * g + 0] + cx[3 * g + 1] * D + cx[3 * g + 2] * D * D;",
+     "uint32_t id = cx[3 * g + 2] + cx[3 * g + 1] * D + cx[3 * g + 0] * D * D;", 1),
+    ("hash cell without the geom offset",
+     "v3 p = vadd(ld3(P4(pos, ga->type_body[1])), ld3(ga->pos_size0));\n        cx[3 * g + 0]",
+     "v3 p = ld3(P4(pos, ga->type_body[1]));\n        cx[3 * g + 0]", 1),
+    ("hash neighbours one-sided in x",
+     "for (int dx = -1; dx <= 1; ++dx)",
+     "for (int dx = 0; dx <= 1; ++dx)", 1),
+    ("hash loop nesting x outermost",
+     "for (int dz = -1; dz <= 1; ++dz) for (int dy = -1; dy <= 1; ++dy) for (int dx = -1; dx <= 1; ++dx) {",
+     "for (int dx = -1; dx <= 1; ++dx) for (int dy = -1; dy <= 1; ++dy) for (int dz = -1; dz <= 1; ++dz) {", 1),
+    ("hash pairs both ways",
+     "if (o <= g) continue;",
+     "if (o == g) continue;", 1),
+    ("hash same-body pairs kept",
+     "                if (body_a == body_b) continue;\n                uint32_t group_b",
+     "                uint32_t group_b", 1),
+    ("hash mask rule and",
+     "if ((group_a & mask_b) == 0 && (group_b & mask_a) == 0) continue;\n                uint32_t type_b",
+     "if ((group_a & mask_b) == 0 || (group_b & mask_a) == 0) continue;\n                uint32_t type_b", 1),
+    ("hash planes take the distance test",
+     "if (!(type_a == 3 || type_b == 3)) {\n                    v3 diff = vsub(pos_b, pos_a);",
+     "if (1) {\n                    v3 diff = vsub(pos_b, pos_a);", 1),
+    ("hash pair written as (o, g)",
+     "                    ct->indices[0] = body_a; ct->indices[1] = body_b; ct->indices[2] = g; ct->indices[3] = o;",
+     "                    ct->indices[0] = body_a; ct->indices[1] = body_b; ct->indices[2] = o; ct->indices[3] = g;", 1),
+    ("hash count stops at M",
+     "uint32_t c = (*count)++;\n                if (c < M) {\n                    ZoContact* ct = &con[c];\n                    ct->indices[0] = body_a; ct->indices[1] = body_b; ct->indices[2] = g;",
+     "uint32_t c = *count;\n                if (c < M) {\n                    ++*count;\n                    ZoContact* ct = &con[c];\n                    ct->indices[0] = body_a; ct->indices[1] = body_b; ct->indices[2] = g;", 1),
 ]
 
 
