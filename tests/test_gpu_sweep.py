@@ -1,0 +1,101 @@
+"""The count-only broad phase of a full contact list, against the oracle bit for bit.
+
+Once a list is full (count >= M; no step clears the count, all_shaders.metal:765-766) and a
+substep cannot wrap the count past 2^32, the one-environment-per-wave kernel only counts the
+listed pairs that pass (:468-533): the pairs with a plane as a model constant, the others by a
+sweep of the non-plane geoms (at most 64) across the wave's lanes. These scenes force one
+environment per wave and a short list, so the sweep runs from the first substep on, with
+bodies of one and two geoms, random contype/conaffinity masks (zero masks included), NaN
+positions, and counts on both sides of the wrap guard (count <= 2^32 - 1 - P).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle.oracle import OracleWorld
+from tests.parity import compare, gpu_arrays, make_pair, oracle_arrays
+from zeno_amd.model import load_model
+from zeno_amd.world import ZenoWorld
+
+pytestmark = pytest.mark.gpu
+
+M = 8
+
+
+def masked_scene(nbodies: int, two_geoms_every: int, seed: int) -> str:
+    rng = np.random.default_rng(seed)
+    lines = ["<mujoco><worldbody>", '<geom type="plane" size="5 5 0.1"/>']
+    for i in range(nbodies):
+        x, y = rng.uniform(-0.6, 0.6, 2)
+        z = rng.uniform(0.05, 1.0)
+        lines.append(f'<body name="b{i}" pos="{x:.3f} {y:.3f} {z:.3f}"><joint type="free"/>')
+        for k in range(2 if (i + 1) % two_geoms_every == 0 else 1):
+            kind = ["sphere", "capsule", "box"][int(rng.integers(0, 3))]
+            size = {"sphere": 1, "capsule": 2, "box": 3}[kind]
+            sz = " ".join(f"{v:.3f}" for v in rng.uniform(0.04, 0.14, size))
+            off = " ".join(f"{v:.3f}" for v in (rng.uniform(-0.1, 0.1, 3) if k else np.zeros(3)))
+            ct, ca = (int(v) for v in rng.integers(0, 4, 2))
+            lines.append(f'<geom type="{kind}" size="{sz}" pos="{off}" contype="{ct}" conaffinity="{ca}"/>')
+        lines.append("</body>")
+    lines.append("</worldbody></mujoco>")
+    return "\n".join(lines)
+
+
+def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M):
+    saved = os.environ.get("ZENO_AMD_ENVS_PER_WAVE")
+    os.environ["ZENO_AMD_ENVS_PER_WAVE"] = "1"
+    try:
+        g = ZenoWorld(mjcf_string=xml, num_envs=envs, max_contacts_per_env=max_contacts)
+    finally:
+        if saved is None:
+            os.environ.pop("ZENO_AMD_ENVS_PER_WAVE")
+        else:
+            os.environ["ZENO_AMD_ENVS_PER_WAVE"] = saved
+    m = load_model(mjcf_string=xml)
+    o = OracleWorld(m, envs, max_contacts_per_env=max_contacts)
+    assert g.launch_config()[0] == 1
+    return m, g, o
+
+
+@pytest.mark.parametrize("nbodies,every,seed", [(40, 3, 0), (30, 1, 1), (64, 1000, 2), (45, 2, 3)])
+def test_sweep_counts_match_oracle(nbodies, every, seed):
+    """40 bodies with every third holding two geoms (53 non-plane geoms), 30 with two each
+    (60), 64 with one (64: the widest sweep), and 45 with every second holding two (67: over
+    64, so the pair loop runs instead); env 2 starts with a NaN position."""
+    xml = masked_scene(nbodies, every, seed)
+    m, g, o = pair_one_env_per_wave(xml, 4)
+    B = m["num_bodies"]
+    state = [np.ascontiguousarray(np.broadcast_to(m[k], (4, B, 4)), np.float32).copy()
+             for k in ("init_positions", "init_quaternions", "init_velocities", "init_angular_velocities")]
+    rng = np.random.default_rng(seed + 10)
+    state[0][:, 1:, :2] += rng.uniform(-0.05, 0.05, (4, B - 1, 2)).astype(np.float32)
+    state[0][2, 3, 0] = np.nan
+    g.reset_to_state(*state)
+    o.reset_to_state(*state)
+    for _ in range(10):
+        g.step(np.zeros((4, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+    assert np.all(o.contact_counts >= M)
+    g.close()
+
+
+def test_sweep_wrap_guard_boundary():
+    """The pile (P = 2080 listed pairs): counts at 2^32 - 1 - P (the last count the sweep
+    takes), one above it (the pair loop), 10 below 2^32 (the pair loop, wrapping) and one far
+    from the wrap."""
+    g, o, acts = make_pair("pile", 4, 6, seed=5, envs_per_wave=1)
+    P = int(o.model["num_pairs"])
+    for k in range(2):
+        g.step(acts[k])
+        o.step(acts[k])
+    top = np.uint64((1 << 32) - 1 - P)
+    counts = np.array([top, top + 1, (1 << 32) - 10, 1000], np.uint64).astype(np.uint32)
+    g.set_contact_counts(counts)
+    o.contact_counts[:] = counts
+    for k in range(2, 6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+    g.close()

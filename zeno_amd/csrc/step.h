@@ -305,6 +305,10 @@ struct StepArgs {
     // 1: sort the contact list in the first substep even if no append took a slot below M (the
     // host changed the counts, exposing slots whose order the last sort did not cover).
     uint32_t sort_all;
+    // Count-only broad phase of a full list (one environment per wave): the non-plane geoms
+    // (sweep_n <= 64, else 0 and the sweep is off) and the number of listed pairs with a plane.
+    const uint32_t* sweep;
+    uint32_t sweep_n, sweep_planes;
     uint32_t iters, substeps;
     // Scalars (SimParams, world.zig:35-56).
     float dt, inv_step, gx, gy, gz, restitution, baumgarte, slop;

@@ -1140,6 +1140,44 @@ void step_kernel(StepArgs a) {
                 if (mine && h > 0 && count + (inc - h) < M) hash_pairs_of<HBM>(a, md, s, hmeta, g, true, count + (inc - h));
                 count += total;
             }
+        } else if (EPW == 1 && live && a.sweep_n != 0u && count >= M && count <= 0xFFFFFFFFu - a.P) {
+            // Count-only sweep. The list is full (count >= M) and this substep cannot wrap
+            // the count past 2^32 (at most P appends), so no append lands below M: the broad
+            // phase only advances the count by the listed pairs that pass (:468-533). Pairs
+            // with a plane always pass (no distance test), so their number is a model constant
+            // (sweep_planes). The other geoms, at most 64 (sweep), sit one per lane; after k
+            // one-lane rotations of the wave each lane holds the geom k lanes along, so
+            // k = 1..32 meets every unordered pair once (k = 32 from the lower half only). Each
+            // pair takes the list's filters (different bodies, contype / conaffinity; the list
+            // holds exactly the pairs passing them, model.cpp) and the same distance test: the
+            // difference's sign does not change its square, nor the radii's order their sum.
+            const bool mine = (uint32_t)sl < a.sweep_n;
+            f3 c = mk3(0.0f, 0.0f, 0.0f);
+            float r = 0.0f;
+            uint32_t body = 0, grp = 0, msk = 0;  // an empty lane passes no mask test
+            if (mine) {
+                const GeomRec& gr = md.geoms[a.sweep[sl]];
+                c = add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2]));
+                r = gr.pos_size0[3];
+                body = gr.type_body[1]; grp = gr.type_body[3]; msk = gr.type_body[2];
+            }
+            auto rol = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x134, 0xF, 0xF, false); };  // wave_rol:1
+            auto rolf = [&](float v) { return __int_as_float((int)rol((uint32_t)__float_as_int(v))); };
+            float px = c.x, py = c.y, pz = c.z, pr = r;
+            uint32_t pb = body, pg = grp, pm = msk, hits = 0;
+#pragma unroll 4
+            for (uint32_t k = 1; k <= 32u; ++k) {
+                px = rolf(px); py = rolf(py); pz = rolf(pz); pr = rolf(pr);
+                pb = rol(pb); pg = rol(pg); pm = rol(pm);
+                const f3 diff = sub(mk3(px, py, pz), c);
+                const float min_dist = r + pr + 0.1f;
+                const bool near = !(dot(diff, diff) >= min_dist * min_dist);  // NaN distances pass, as in :521
+                const bool listed = body != pb && ((grp & pm) != 0u || (pg & msk) != 0u);
+                const bool once = k < 32u || (uint32_t)sl < 32u;
+                hits += (near && listed && once) ? 1u : 0u;
+            }
+            for (uint32_t d = 1; d < 64u; d <<= 1) hits += (uint32_t)__shfl_xor((int)hits, (int)d);
+            count += a.sweep_planes + hits;
         } else {
             const uint64_t group_mask = (G == 64) ? ~0ull : (((1ull << (G % 64)) - 1ull) << (le * G));
             const uint64_t below = (sl == 0) ? 0ull : ((~0ull) >> (64 - sl)) << (le * G);

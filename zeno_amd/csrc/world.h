@@ -60,6 +60,10 @@ struct World {
     ContactRec* d_con = nullptr;
     uint32_t *d_counts = nullptr, *d_pcounts = nullptr;
     uint32_t* d_cell_ids = nullptr;       // [E*G] hash mode
+    // Count-only sweep of a full list: the non-plane geoms (at most 64; none when the scene
+    // is hashed or has more) and the number of listed pairs with a plane.
+    uint32_t* d_sweep = nullptr;
+    uint32_t sweep_n = 0, sweep_planes = 0;
     unsigned char* d_work = nullptr;      // [E * lds.bytes] HBM working sets
     // step_subset support, allocated on first use.
     ContactRec* d_prev_con = nullptr;

@@ -94,7 +94,7 @@ World::~World() {
     release_graph();
     void* dev[] = {d_model, d_phase, d_init_pos, d_init_quat, d_init_vel, d_init_angvel, d_pos, d_quat, d_vel, d_angvel, d_acc,
                    d_jpos, d_jvel, d_jtrq, d_obs, d_lam, d_actions, d_con, d_counts, d_pcounts, d_prev_con,
-                   d_prev_detached, d_mask, d_stage, d_cell_ids, d_work};
+                   d_prev_detached, d_mask, d_stage, d_cell_ids, d_work, d_sweep};
     for (void* p : dev) if (p) hipFree(p);
     for (int i = 0; i < MIR_COUNT_ALL; ++i) if (h_mirror[i]) hipHostFree(h_mirror[i]);
     for (int i = 0; i < kStage; ++i) {
@@ -295,6 +295,17 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         put(w->ml.bjl, bjl.data(), 4 * bjl.size());
         if ((e = upload(w, &w->d_model, (const uint4*)blob.data(), w->ml.bytes / 16)) != hipSuccess) return fail("upload", e);
     }
+    if (!w->hash && !m.pairs.empty()) {
+        std::vector<uint32_t> sweep;
+        for (uint32_t g = 0; g < m.num_geoms; ++g) if (m.geoms[g].type_body[0] != GEOM_PLANE) sweep.push_back(g);
+        if (!sweep.empty() && sweep.size() <= 64) {
+            for (uint32_t pr : m.pairs) {
+                if (m.geoms[pr & 0xFFFFu].type_body[0] == GEOM_PLANE || m.geoms[pr >> 16].type_body[0] == GEOM_PLANE) ++w->sweep_planes;
+            }
+            w->sweep_n = (uint32_t)sweep.size();
+            if ((e = upload(w, &w->d_sweep, sweep.data(), sweep.size())) != hipSuccess) return fail("upload", e);
+        }
+    }
     std::vector<float4> ip(w->B), iq(w->B), iv(w->B), ia(w->B);
     for (uint32_t b = 0; b < w->B; ++b) {
         ip[b] = make_float4(m.init_pos[4 * b], m.init_pos[4 * b + 1], m.init_pos[4 * b + 2], m.init_pos[4 * b + 3]);
@@ -388,6 +399,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.cell_ids = d_cell_ids;
     a.ext_contacts = ext_contacts ? 1u : 0u;
     a.sort_all = resort ? 1u : 0u;
+    a.sweep = d_sweep; a.sweep_n = sweep_n; a.sweep_planes = sweep_planes;
     resort = false;
     a.placement = placement;
     a.work = d_work;
