@@ -42,9 +42,9 @@ def masked_scene(nbodies: int, two_geoms_every: int, seed: int) -> str:
     return "\n".join(lines)
 
 
-def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M):
+def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M, epw: int = 1):
     saved = os.environ.get("ZENO_AMD_ENVS_PER_WAVE")
-    os.environ["ZENO_AMD_ENVS_PER_WAVE"] = "1"
+    os.environ["ZENO_AMD_ENVS_PER_WAVE"] = str(epw)
     try:
         g = ZenoWorld(mjcf_string=xml, num_envs=envs, max_contacts_per_env=max_contacts)
     finally:
@@ -54,8 +54,35 @@ def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M):
             os.environ["ZENO_AMD_ENVS_PER_WAVE"] = saved
     m = load_model(mjcf_string=xml)
     o = OracleWorld(m, envs, max_contacts_per_env=max_contacts)
-    assert g.launch_config()[0] == 1
+    assert g.launch_config()[0] == epw
     return m, g, o
+
+
+def hinged_row(n: int) -> str:
+    """n capsules hinged to the world body over a plane, swinging under gravity."""
+    lines = ["<mujoco><worldbody>", '<geom type="plane" size="5 5 0.1"/>']
+    for i in range(n):
+        lines.append(f'<body name="p{i}" pos="{0.3 * i:.2f} 0 1"><joint type="hinge" axis="0 1 0"/>'
+                     f'<geom type="capsule" size="0.05 0.3" pos="0.2 0 0" quat="0.7071 0 0.7071 0"/></body>')
+    lines.append("</worldbody></mujoco>")
+    return "\n".join(lines)
+
+
+@pytest.mark.parametrize("scene,epw", [("free32", 2), ("free16", 4), ("hinged16", 4), ("hinged64", 1)])
+def test_static_world_body_set_aside(scene, epw):
+    """Scenes whose bodies after the world body fill whole passes of an environment's lanes
+    (B - 1 = 64 / EPW or 64): the per-body stages take bodies 1.. across the lanes and set the
+    static world body aside. Free bodies, and bodies hinged to the world (whose joints read
+    the world body's pose), every step against the oracle."""
+    xml = {"free32": masked_scene(32, 1000, 7), "free16": masked_scene(16, 1000, 8),
+           "hinged16": hinged_row(16), "hinged64": hinged_row(64)}[scene]
+    m, g, o = pair_one_env_per_wave(xml, 8, max_contacts=16, epw=epw)
+    assert (m["num_bodies"] - 1) % (64 // epw) == 0
+    for _ in range(12):
+        g.step(np.zeros((8, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+    g.close()
 
 
 @pytest.mark.parametrize("nbodies,every,seed", [(40, 3, 0), (30, 1, 1), (64, 1000, 2), (45, 2, 3)])

@@ -348,6 +348,11 @@ struct StepArgs {
     unsigned char* work;            // PL_ALL_HBM, PL_WORK_HBM: lds.bytes per environment; else null
     EnvLds lds;
     EnvLds lds_small;               // PL_ALL_HBM: the arrays kept in LDS (make_env_lds_small)
+    // 1: body 0 is static (inverse mass < 1e-8) and not kinematic, and the bodies after it fill
+    // whole passes of an environment's lanes. Its forces are zero, its previous pose is its
+    // pose, and it is neither integrated nor given a velocity update, so the per-body stages
+    // of the unsplit shapes take bodies 1.. across the lanes and set body 0's entries aside.
+    uint32_t b_first;
 };
 
 // Where the step kernel keeps the model records and each environment's working set.

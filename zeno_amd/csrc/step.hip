@@ -831,7 +831,13 @@ void step_kernel(StepArgs a) {
     const size_t eb = (size_t)env * B;
     const ContactRec* gc = a.contacts + (size_t)env * M;
     const uint32_t b0 = sl, j0 = sl;
+    // One environment per workgroup with the model records in HBM: a second body per lane is
+    // read ahead as well, so scenes of up to 2 G bodies (the pile's 65) load in one round trip.
+    constexpr bool PRE2 = EPW == 1 && PL == PL_MODEL_HBM && !HASH;
+    // Split groups keep every body on the lanes (their solver chain gains nothing from it).
+    const uint32_t bf = SPLIT ? 0u : a.b_first;
     float4 p_pos = make_float4(0, 0, 0, 0), p_quat = p_pos, p_vel = p_pos, p_ang = p_pos;
+    float4 q_pos = p_pos, q_quat = p_pos, q_vel = p_pos, q_ang = p_pos;
     float p_jt = 0.0f, p_lam = 0.0f;
     Slot4 c0{}, c1{}, c2{}, c3{};
     if (live && do_solve) {
@@ -840,6 +846,12 @@ void step_kernel(StepArgs a) {
             p_quat = a.quat[eb + b0];
             p_vel = a.vel[eb + b0];
             p_ang = a.angvel[eb + b0];
+        }
+        if (PRE2 && b0 + G < B) {
+            q_pos = a.pos[eb + b0 + G];
+            q_quat = a.quat[eb + b0 + G];
+            q_vel = a.vel[eb + b0 + G];
+            q_ang = a.angvel[eb + b0 + G];
         }
         if (j0 < Jp) p_jt = a.jtrq[(size_t)env * Jp + j0];
         if (j0 < N) p_lam = a.lam[(size_t)env * N + j0];
@@ -883,10 +895,17 @@ void step_kernel(StepArgs a) {
         const uint4* src = a.model + a.ml.jrec / 16u;
         for (uint32_t i = tid; i < a.nrec * kJRecQuads; i += kWave) ((uint4*)s.jrec)[i] = src[i];
         if (!HASH) {
-            for (uint32_t g = tid; g < a.G; g += kWave) {
-                const GeomRec& gr = md.geoms[g];
-                s.gst[g] = make_float4(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2], gr.pos_size0[3]);
-                s.gmeta[g] = gr.type_body[1] | (gr.type_body[0] << 16);
+            // Two geoms per lane and trip, both read before either is written.
+            for (uint32_t g = tid; g < a.G; g += 2u * kWave) {
+                const uint32_t g2 = g + kWave;
+                const float4 ps = *(const float4*)md.geoms[g].pos_size0;
+                const uint4 tb = *(const uint4*)md.geoms[g].type_body;
+                float4 ps2 = ps;
+                uint4 tb2 = tb;
+                if (g2 < a.G) { ps2 = *(const float4*)md.geoms[g2].pos_size0; tb2 = *(const uint4*)md.geoms[g2].type_body; }
+                s.gst[g] = ps;
+                s.gmeta[g] = tb.y | (tb.x << 16);
+                if (g2 < a.G) { s.gst[g2] = ps2; s.gmeta[g2] = tb2.y | (tb2.x << 16); }
             }
         }
     }
@@ -917,7 +936,14 @@ void step_kernel(StepArgs a) {
             s.vb[b0] = p_vel;
             s.angvel[b0] = p_ang;
         }
-        for (uint32_t b = sl + G; b < B; b += G) {
+        if (PRE2 && b0 + G < B) {
+            s.pos[b0 + G] = q_pos;
+            s.quat[b0 + G] = q_quat;
+            s.vel[b0 + G] = q_vel;
+            s.vb[b0 + G] = q_vel;
+            s.angvel[b0 + G] = q_ang;
+        }
+        for (uint32_t b = sl + (PRE2 ? 2u : 1u) * G; b < B; b += G) {
             s.pos[b] = a.pos[eb + b];
             s.quat[b] = a.quat[eb + b];
             float4 v = a.vel[eb + b];
@@ -975,7 +1001,13 @@ void step_kernel(StepArgs a) {
                 float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
                 s.jt[(uint32_t)act.params[0]] = torque;
             }
-            for (uint32_t b = sl; b < B; b += G) {
+            if (bf != 0u && sl == 0) {
+                s.frc[0] = make_float4(0, 0, 0, 0);
+                s.trq[0] = make_float4(0, 0, 0, 0);
+                s.ppos[0] = s.pos[0];
+                s.pquat[0] = s.quat[0];
+            }
+            for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
                 float4 P = s.pos[b], Q = s.quat[b];
                 if (imi.x < 1e-8f) {
@@ -1020,7 +1052,7 @@ void step_kernel(StepArgs a) {
         wave_sync<HBM>();
         // ---- D: integrate (:394-462), on the lane that formed the body's forces -----------
         if (live && do_solve) {
-            for (uint32_t b = sl; b < B; b += G) {
+            for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
                 if (imi.x < 1e-8f) {
                     if (SPLIT) { s.frc[b] = s.pos[b]; s.trq[b] = s.quat[b]; }  // the helper's pose copy
@@ -1773,7 +1805,7 @@ void step_kernel(StepArgs a) {
         // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
         if (live && do_solve) {
             const float inv_dt = 1.0f / a.dt;
-            for (uint32_t b = sl; b < B; b += G) {
+            for (uint32_t b = bf + sl; b < B; b += G) {
                 if (md.invmi[b].x < 1e-8f) continue;
                 s.vel[b] = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
                 q4 dq = qmul(toq(s.quat[b]), qconj(toq(s.pquat[b])));

@@ -64,6 +64,7 @@ struct World {
     // is hashed or has more) and the number of listed pairs with a plane.
     uint32_t* d_sweep = nullptr;
     uint32_t sweep_n = 0, sweep_planes = 0;
+    bool b0_static = false;  // body 0 is static and not kinematic (the per-body stages may skip it)
     unsigned char* d_work = nullptr;      // [E * lds.bytes] HBM working sets
     // step_subset support, allocated on first use.
     ContactRec* d_prev_con = nullptr;

@@ -162,6 +162,7 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
         flags[b] = ((uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u) | (im[0] > 1e-8f ? 2u : 0u);
     }
+    w->b0_static = w->B > 1 && invmi[0].x < 1e-8f && (flags[0] & 1u) == 0u;
     std::vector<float4> jrec;
     std::vector<JointPhase> jph;
     build_joint_program(m.templates, m.color_ranges, (const float*)invmi.data(), (const float*)com.data(), jrec, jph);
@@ -400,6 +401,8 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.ext_contacts = ext_contacts ? 1u : 0u;
     a.sort_all = resort ? 1u : 0u;
     a.sweep = d_sweep; a.sweep_n = sweep_n; a.sweep_planes = sweep_planes;
+    // Only where it saves a pass: the bodies after body 0 fill whole passes of the lanes.
+    a.b_first = (b0_static && (B - 1u) % (64u / (uint32_t)epw) == 0u) ? 1u : 0u;
     resort = false;
     a.placement = placement;
     a.work = d_work;
