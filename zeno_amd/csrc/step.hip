@@ -793,6 +793,18 @@ void step_kernel(StepArgs a) {
     if (PL != PL_LDS) md.jrec = s.jrec;
     const uint32_t B = a.B, M = a.M, N = a.N, Jp = a.Jp;
     const bool stepped = live && (a.step_mask == nullptr || a.step_mask[env] != 0);
+    // Working sets in HBM: an advanced environment's pose and velocity arrays are its slices
+    // of the state arrays themselves (the same layout), so they are neither copied in nor
+    // written back. An environment that is not advanced keeps its visible state and works on
+    // copies in the working set, as the other placements do.
+    const bool alias = HBM && stepped;
+    // Aliased and with no host view held, the last substep's velocity update writes each
+    // dynamic body's acceleration itself (the write-back then covers the static bodies only).
+    const bool j_acc = alias && !a.hv.pos && !a.hv.quat && !a.hv.vel && !a.hv.angvel && !a.hv.acc;
+    if (alias) {
+        const size_t eb0 = (size_t)env * a.B;
+        s.pos = a.pos + eb0; s.quat = a.quat + eb0; s.vel = a.vel + eb0; s.angvel = a.angvel + eb0;
+    }
 
     // Phase timer: workgroup 0, lane 0 accumulates wall-clock ticks per phase.
     const bool timer = a.phase_ticks != nullptr && blockIdx.x == 0 && threadIdx.x == 0;
@@ -842,10 +854,12 @@ void step_kernel(StepArgs a) {
     Slot4 c0{}, c1{}, c2{}, c3{};
     if (live && do_solve) {
         if (b0 < B) {
-            p_pos = a.pos[eb + b0];
-            p_quat = a.quat[eb + b0];
             p_vel = a.vel[eb + b0];
-            p_ang = a.angvel[eb + b0];
+            if (!alias) {
+                p_pos = a.pos[eb + b0];
+                p_quat = a.quat[eb + b0];
+                p_ang = a.angvel[eb + b0];
+            }
         }
         if (PRE2 && b0 + G < B) {
             q_pos = a.pos[eb + b0 + G];
@@ -930,11 +944,13 @@ void step_kernel(StepArgs a) {
 
     if (live && do_solve) {
         if (b0 < B) {
-            s.pos[b0] = p_pos;
-            s.quat[b0] = p_quat;
-            s.vel[b0] = p_vel;
+            if (!alias) {
+                s.pos[b0] = p_pos;
+                s.quat[b0] = p_quat;
+                s.vel[b0] = p_vel;
+                s.angvel[b0] = p_ang;
+            }
             s.vb[b0] = p_vel;
-            s.angvel[b0] = p_ang;
         }
         if (PRE2 && b0 + G < B) {
             s.pos[b0 + G] = q_pos;
@@ -944,12 +960,14 @@ void step_kernel(StepArgs a) {
             s.angvel[b0 + G] = q_ang;
         }
         for (uint32_t b = sl + (PRE2 ? 2u : 1u) * G; b < B; b += G) {
-            s.pos[b] = a.pos[eb + b];
-            s.quat[b] = a.quat[eb + b];
-            float4 v = a.vel[eb + b];
-            s.vel[b] = v;
+            const float4 v = a.vel[eb + b];
+            if (!alias) {
+                s.pos[b] = a.pos[eb + b];
+                s.quat[b] = a.quat[eb + b];
+                s.vel[b] = v;
+                s.angvel[b] = a.angvel[eb + b];
+            }
             s.vb[b] = v;
-            s.angvel[b] = a.angvel[eb + b];
         }
         if (j0 < Jp) s.jt[j0] = p_jt;
         if (j0 < N) s.lam[j0] = p_lam;
@@ -988,19 +1006,8 @@ void step_kernel(StepArgs a) {
             }
         };
         if (!SPLIT && live) snapshot();
-        // ---- A + B: warm_start_constraints, apply_actions (:1408-1426, :196-229), then per
-        // body compute_forces and update_kinematic in dispatch order (:345-388, :304-339,
-        // world.zig:962-990: the torque reads the quaternion before a kinematic body's
-        // update) and save_prev_state (:1900-1913). Each lane touches only its own entries.
-        if (live && do_solve) {
-            for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
-            for (uint32_t k = sl; k < a.A; k += G) {
-                const ActuatorRec& act = md.acts[k];
-                const float av = k == (uint32_t)sl ? act0 : a.actions[(size_t)env * a.A + k];
-                float ctrl = clampf(av, act.params[1], act.params[2]);
-                float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
-                s.jt[(uint32_t)act.params[0]] = torque;
-            }
+        // Stage B (below), one text for the two places it runs from.
+        auto stage_b = [&]() {
             if (bf != 0u && sl == 0) {
                 s.frc[0] = make_float4(0, 0, 0, 0);
                 s.trq[0] = make_float4(0, 0, 0, 0);
@@ -1031,13 +1038,84 @@ void step_kernel(StepArgs a) {
                 s.ppos[b] = P;
                 s.pquat[b] = Q;
             }
+        };
+        // ---- A + B: warm_start_constraints, apply_actions (:1408-1426, :196-229), then per
+        // body compute_forces and update_kinematic in dispatch order (:345-388, :304-339,
+        // world.zig:962-990: the torque reads the quaternion before a kinematic body's
+        // update) and save_prev_state (:1900-1913). Each lane touches only its own entries.
+        if (live && do_solve) {
+            for (uint32_t i = sl; i < N; i += G) s.lam[i] = 0.8f * s.lam[i];
+            for (uint32_t k = sl; k < a.A; k += G) {
+                const ActuatorRec& act = md.acts[k];
+                const float av = k == (uint32_t)sl ? act0 : a.actions[(size_t)env * a.A + k];
+                float ctrl = clampf(av, act.params[1], act.params[2]);
+                float torque = clampf(ctrl * act.params[3], act.params2[0], act.params2[1]);
+                s.jt[(uint32_t)act.params[0]] = torque;
+            }
+            if (!HBM) stage_b();
         }
+        // Working sets in HBM, one environment per wave: when no joint contributes a force
+        // (every |tau| < 1e-6, so stage C adds nothing), each body's forces feed its own
+        // integration at once, in registers (the same operations as B then D), and the force,
+        // torque and contribution arrays are neither written nor read.
+        bool fuse = false;
+        if (HBM) {
+            wave_sync<HBM>();  // the torques apply_actions wrote
+            bool contrib = false;
+            if (live && do_solve) {
+                for (uint32_t j = sl; j < a.J; j += G) contrib = contrib || !(__builtin_fabsf(s.jt[j]) < 1e-6f);
+            }
+            fuse = __ballot(contrib) == 0ull;
+        }
+        if (HBM && live && do_solve && fuse) {
+            if (bf != 0u && sl == 0) {
+                s.ppos[0] = s.pos[0];
+                s.pquat[0] = s.quat[0];
+            }
+            for (uint32_t b = bf + sl; b < B; b += G) {
+                const float4 imi = md.invmi[b];
+                float4 P = s.pos[b], Q = s.quat[b];
+                const bool dyn = !(imi.x < 1e-8f);
+                f3 force = mk3(0.0f, 0.0f, 0.0f), torque = force;
+                if (dyn) {
+                    float mass = 1.0f / imi.x;
+                    force = mk3(a.gx * mass, a.gy * mass, a.gz * mass);
+                    f3 cw = qrot(xyz(md.com[b]), toq(Q));
+                    torque = cross(cw, force);
+                }
+                if (md.flags[b] & 1u) {
+                    P = tof4(add(xyz(P), scale(xyz(s.vel[b]), a.dt)), 0.0f);
+                    const q4 q = toq(Q);
+                    f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
+                    Q = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
+                    s.pos[b] = P;
+                    s.quat[b] = Q;
+                }
+                s.ppos[b] = P;
+                s.pquat[b] = Q;
+                if (!dyn) continue;
+                f3 vel = add(xyz(s.vel[b]), scale(scale(force, imi.x), a.dt));
+                vel = scale(vel, 0.999f);
+                f3 pos = add(xyz(P), scale(vel, a.dt));
+                s.vel[b] = tof4(vel, 0.0f);
+                s.pos[b] = tof4(pos, 0.0f);
+                f3 om = add(xyz(s.angvel[b]), scale(mul(mk3(imi.y, imi.z, imi.w), torque), a.dt));
+                om = scale(om, 0.999f);
+                q4 q = toq(Q);
+                f3 h = scale(scale(om, a.dt), 0.5f);
+                q = qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q));
+                q = qnormalize(q);
+                s.angvel[b] = tof4(om, 0.0f);
+                s.quat[b] = tof4(q);
+            }
+        }
+        if (HBM && live && do_solve && !fuse) stage_b();
         wave_sync<HBM>();
         // ---- C: apply_joint_forces (S2, :122-190) -------------------------------------
         // Each joint's world-frame contribution axis_world * tau is formed by one lane into
         // jw (skipped when |tau| < 1e-6, flag w = 0); then each body sums the contributions
         // of its joints in ascending joint order (build_body_joint_lists), and integrates.
-        if (live && do_solve) {
+        if (live && do_solve && !fuse) {
             for (uint32_t j = sl; j < a.J; j += G) {
                 const JointRec& jr = md.joints[j];
                 const float tau = s.jt[j];
@@ -1051,7 +1129,7 @@ void step_kernel(StepArgs a) {
         }
         wave_sync<HBM>();
         // ---- D: integrate (:394-462), on the lane that formed the body's forces -----------
-        if (live && do_solve) {
+        if (live && do_solve && !fuse) {
             for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
                 if (imi.x < 1e-8f) {
@@ -1805,12 +1883,18 @@ void step_kernel(StepArgs a) {
         // ---- J: xpbd_update_velocities (:1922-1961) ----------------------------------
         if (live && do_solve) {
             const float inv_dt = 1.0f / a.dt;
+            const bool acc_here = j_acc && step + 1 == a.substeps;
             for (uint32_t b = bf + sl; b < B; b += G) {
                 if (md.invmi[b].x < 1e-8f) continue;
-                s.vel[b] = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
+                const float4 v = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
+                s.vel[b] = v;
                 q4 dq = qmul(toq(s.quat[b]), qconj(toq(s.pquat[b])));
                 if (dq.w < 0) dq = qneg(dq);
                 s.angvel[b] = tof4(scale(sscale(2.0f, xyz(dq)), inv_dt), 0.0f);
+                if (acc_here) {
+                    const float4 v0 = s.vb[b];
+                    a.acc[(size_t)env * B + b] = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+                }
             }
         }
         wave_sync<HBM>();
@@ -1821,14 +1905,19 @@ void step_kernel(StepArgs a) {
                 const uint32_t type = (uint32_t)jr.params[0];
                 const uint32_t ja = (uint32_t)jr.params[1], jb = (uint32_t)jr.params[2];
                 float jp = 0.0f, jv = 0.0f;
-                const q4 q_a = toq(s.quat[ja]), q_b = toq(s.quat[jb]);
+                // Working sets in HBM: the orientations are read only by the joint types that
+                // use them.
+                q4 q_a = mk4(0.0f, 0.0f, 0.0f, 1.0f), q_b = q_a;
+                if (!HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
                 if (type == JOINT_REVOLUTE) {
+                    if (HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
                     const f3 axis_local = mk3(jr.axis[0], jr.axis[1], jr.axis[2]);
                     const f3 aw = qrot(axis_local, q_a);
                     const q4 q_rel = qmul(qconj(q_a), q_b);
                     jp = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
                     jv = dot(sub(xyz(s.angvel[jb]), xyz(s.angvel[ja])), aw);
                 } else if (type == JOINT_PRISMATIC) {
+                    if (HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
                     const f3 aw = qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), q_a);
                     const f3 r_a = qrot(mk3(jr.anchor_parent[0], jr.anchor_parent[1], jr.anchor_parent[2]), q_a);
                     const f3 r_b = qrot(mk3(jr.anchor_child[0], jr.anchor_child[1], jr.anchor_child[2]), q_b);
@@ -1881,6 +1970,10 @@ void step_kernel(StepArgs a) {
         const size_t eb = (size_t)env * B;
         const StepArgs::HostViews& hv = a.hv;
         if (do_solve) {
+        // With the pose arrays aliased on the state, only the accelerations (and any held
+        // views) are written, so the pose reads are skipped when no view needs them.
+        const bool pose_out = !alias || hv.pos || hv.quat || hv.angvel;
+        if (!HBM) {
         for (uint32_t b = sl; b < B; b += G) {
             const float4 p = s.pos[b], q = s.quat[b], v = s.vel[b], v0 = s.vb[b], w = s.angvel[b];
             const float4 acc = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
@@ -1895,6 +1988,28 @@ void step_kernel(StepArgs a) {
             if (hv.angvel) hv.angvel[eb + b] = w;
             if (hv.acc) hv.acc[eb + b] = acc;
         }
+        } else {
+        for (uint32_t b = sl; b < B; b += G) {
+            if (j_acc && !(md.invmi[b].x < 1e-8f)) continue;  // written by the velocity update
+            const float4 v = s.vel[b], v0 = s.vb[b];
+            const float4 acc = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+            a.acc[eb + b] = acc;
+            if (hv.vel) hv.vel[eb + b] = v;
+            if (hv.acc) hv.acc[eb + b] = acc;
+            if (pose_out) {
+                const float4 p = s.pos[b], q = s.quat[b], w = s.angvel[b];
+                if (!alias) {
+                    a.pos[eb + b] = p;
+                    a.quat[eb + b] = q;
+                    a.vel[eb + b] = v;
+                    a.angvel[eb + b] = w;
+                }
+                if (hv.pos) hv.pos[eb + b] = p;
+                if (hv.quat) hv.quat[eb + b] = q;
+                if (hv.angvel) hv.angvel[eb + b] = w;
+            }
+        }
+        }  // HBM
         for (uint32_t j = sl; j < a.J; j += G) {
             const size_t o = (size_t)env * Jp + j;
             a.jtrq[o] = s.jt[j];
