@@ -853,13 +853,11 @@ void step_kernel(StepArgs a) {
     float p_jt = 0.0f, p_lam = 0.0f;
     Slot4 c0{}, c1{}, c2{}, c3{};
     if (live && do_solve) {
-        if (b0 < B) {
+        if (b0 < B && !alias) {
             p_vel = a.vel[eb + b0];
-            if (!alias) {
-                p_pos = a.pos[eb + b0];
-                p_quat = a.quat[eb + b0];
-                p_ang = a.angvel[eb + b0];
-            }
+            p_pos = a.pos[eb + b0];
+            p_quat = a.quat[eb + b0];
+            p_ang = a.angvel[eb + b0];
         }
         if (PRE2 && b0 + G < B) {
             q_pos = a.pos[eb + b0 + G];
@@ -943,14 +941,12 @@ void step_kernel(StepArgs a) {
     }
 
     if (live && do_solve) {
-        if (b0 < B) {
-            if (!alias) {
-                s.pos[b0] = p_pos;
-                s.quat[b0] = p_quat;
-                s.vel[b0] = p_vel;
-                s.angvel[b0] = p_ang;
-            }
+        if (b0 < B && !alias) {  // aliased: the velocity at call start is taken by stage B of substep 0
+            s.pos[b0] = p_pos;
+            s.quat[b0] = p_quat;
+            s.vel[b0] = p_vel;
             s.vb[b0] = p_vel;
+            s.angvel[b0] = p_ang;
         }
         if (PRE2 && b0 + G < B) {
             s.pos[b0 + G] = q_pos;
@@ -959,15 +955,13 @@ void step_kernel(StepArgs a) {
             s.vb[b0 + G] = q_vel;
             s.angvel[b0 + G] = q_ang;
         }
-        for (uint32_t b = sl + (PRE2 ? 2u : 1u) * G; b < B; b += G) {
-            const float4 v = a.vel[eb + b];
-            if (!alias) {
-                s.pos[b] = a.pos[eb + b];
-                s.quat[b] = a.quat[eb + b];
-                s.vel[b] = v;
-                s.angvel[b] = a.angvel[eb + b];
-            }
+        for (uint32_t b = sl + (PRE2 ? 2u : 1u) * G; b < B && !alias; b += G) {
+            s.pos[b] = a.pos[eb + b];
+            s.quat[b] = a.quat[eb + b];
+            float4 v = a.vel[eb + b];
+            s.vel[b] = v;
             s.vb[b] = v;
+            s.angvel[b] = a.angvel[eb + b];
         }
         if (j0 < Jp) s.jt[j0] = p_jt;
         if (j0 < N) s.lam[j0] = p_lam;
@@ -1007,16 +1001,19 @@ void step_kernel(StepArgs a) {
         };
         if (!SPLIT && live) snapshot();
         // Stage B (below), one text for the two places it runs from.
+        const bool take_vb = alias && step == 0;  // aliased: the velocity at call start
         auto stage_b = [&]() {
             if (bf != 0u && sl == 0) {
                 s.frc[0] = make_float4(0, 0, 0, 0);
                 s.trq[0] = make_float4(0, 0, 0, 0);
                 s.ppos[0] = s.pos[0];
                 s.pquat[0] = s.quat[0];
+                if (take_vb) s.vb[0] = s.vel[0];
             }
             for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
                 float4 P = s.pos[b], Q = s.quat[b];
+                if (take_vb) s.vb[b] = s.vel[b];
                 if (imi.x < 1e-8f) {
                     s.frc[b] = make_float4(0, 0, 0, 0);
                     s.trq[b] = make_float4(0, 0, 0, 0);
@@ -1071,10 +1068,13 @@ void step_kernel(StepArgs a) {
             if (bf != 0u && sl == 0) {
                 s.ppos[0] = s.pos[0];
                 s.pquat[0] = s.quat[0];
+                if (take_vb) s.vb[0] = s.vel[0];
             }
             for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
                 float4 P = s.pos[b], Q = s.quat[b];
+                const float4 V = s.vel[b];
+                if (take_vb) s.vb[b] = V;
                 const bool dyn = !(imi.x < 1e-8f);
                 f3 force = mk3(0.0f, 0.0f, 0.0f), torque = force;
                 if (dyn) {
@@ -1084,7 +1084,7 @@ void step_kernel(StepArgs a) {
                     torque = cross(cw, force);
                 }
                 if (md.flags[b] & 1u) {
-                    P = tof4(add(xyz(P), scale(xyz(s.vel[b]), a.dt)), 0.0f);
+                    P = tof4(add(xyz(P), scale(xyz(V), a.dt)), 0.0f);
                     const q4 q = toq(Q);
                     f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
                     Q = tof4(qnormalize(qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q))));
@@ -1094,7 +1094,7 @@ void step_kernel(StepArgs a) {
                 s.ppos[b] = P;
                 s.pquat[b] = Q;
                 if (!dyn) continue;
-                f3 vel = add(xyz(s.vel[b]), scale(scale(force, imi.x), a.dt));
+                f3 vel = add(xyz(V), scale(scale(force, imi.x), a.dt));
                 vel = scale(vel, 0.999f);
                 f3 pos = add(xyz(P), scale(vel, a.dt));
                 s.vel[b] = tof4(vel, 0.0f);
