@@ -1,4 +1,4 @@
-"""The count-only broad phase of a full contact list, against the oracle bit for bit.
+"""The count-only broad phases of a full contact list, against the oracle bit for bit.
 
 Once a list is full (count >= M; no step clears the count, all_shaders.metal:765-766) and a
 substep cannot wrap the count past 2^32, the one-environment-per-wave kernel only counts the
@@ -6,7 +6,8 @@ listed pairs that pass (:468-533): the pairs with a plane as a model constant, t
 sweep of the non-plane geoms (at most 64) across the wave's lanes. These scenes force one
 environment per wave and a short list, so the sweep runs from the first substep on, with
 bodies of one and two geoms, random contype/conaffinity masks (zero masks included), NaN
-positions, and counts on both sides of the wrap guard (count <= 2^32 - 1 - P).
+positions, and counts on both sides of the wrap guard (count <= 2^32 - 1 - P). The spatial
+hash has a count-only form as well (its last test).
 """
 import os
 
@@ -125,4 +126,36 @@ def test_sweep_wrap_guard_boundary():
         g.step(acts[k])
         o.step(acts[k])
         compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-5, atol=1e-6)
+    g.close()
+
+
+def test_hash_count_only_matches_oracle():
+    """The spatial hash's count-only queries (a full list, no wrap possible this substep:
+    count <= 2^32 - 1 - G (G - 1) / 2): the 600-body hash pile with a 16-slot list, env 1's
+    bodies crowded into the clamped corner cells (long runs, dealt out across the wave), env 2
+    with NaN positions, and counts on both sides of the wrap guard, every step against the
+    oracle."""
+    g, o, acts = make_pair("pile_hash", 4, 8, seed=11, max_contacts=16)
+    B = o.B
+    state = [o.positions.copy(), o.quaternions.copy(), o.velocities.copy(), o.angular_velocities.copy()]
+    rng = np.random.default_rng(12)
+    state[0][1, 1:201, :2] = rng.uniform(-4.0, 0.9, (200, 2)).astype(np.float32)
+    state[0][2, 5:9, 0] = np.nan
+    g.reset_to_state(*state)
+    o.reset_to_state(*state)
+    g.step(acts[0])
+    o.step(acts[0])
+    compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    G = int(o.model["num_geoms"])
+    top = np.uint64((1 << 32) - 1 - G * (G - 1) // 2)
+    counts = o.contact_counts.astype(np.uint64)
+    counts[0], counts[3] = top, top + 1
+    counts = counts.astype(np.uint32)
+    g.set_contact_counts(counts)
+    o.contact_counts[:] = counts
+    for k in range(1, 8):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    assert np.all(o.contact_counts[1:3] >= 16)
     g.close()

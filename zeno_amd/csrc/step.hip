@@ -550,7 +550,7 @@ __device__ __forceinline__ void solve_contact2(const Mdl& md, const Lds& s, uint
 // ---------------------------------------------------------------------------------------
 // narrow_phase, all_shaders.metal:751-894, one slot.
 // ---------------------------------------------------------------------------------------
-__device__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* c) {
+__device__ __forceinline__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* c) {
     const uint32_t body_a = c->indices[0], body_b = c->indices[1];
     const GeomRec& ga = md.geoms[c->indices[2]];
     const GeomRec& gb = md.geoms[c->indices[3]];
@@ -691,7 +691,7 @@ __device__ __forceinline__ uint4 hash_geom_meta(const Mdl& md, const uint4* hmet
 }
 
 template <bool STAGED>
-__device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, uint32_t g, bool emit,
+__device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, uint32_t g, bool emit,
                                   uint32_t slot) {
     const float4 pa4 = hash_geom_pos<STAGED>(md, s, g);
     const uint4 ma = hash_geom_meta<STAGED>(md, hmeta, g);
@@ -733,6 +733,138 @@ __device__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s
             }
         }
     }
+    return hits;
+}
+
+// Count-only hash queries (one environment per wave, a full contact list): the number of
+// pairs the queries above would append, without their order. Each unordered pair of geoms in
+// adjacent cells is met once, from the earlier of the two in the sorted key list: there the
+// other is in the same cell or in one of the 13 adjacent cells of larger id (dx + 64 dy +
+// 4096 dz > 0), i.e. in five runs of the list: the rest of the cell and the cell at x + 1,
+// the row y + 1 at z, and the rows y - 1, y, y + 1 at z + 1 (x - 1 .. x + 1 each). The pair
+// tests are those of hash_pairs_of; each is symmetric in its two geoms (the difference's
+// sign does not change its square, nor the radii's order their sum), so the earlier geom
+// may take either role. The runs' nine ends are found by interleaved binary searches, then
+// the wave's candidates are dealt out 64 at a time, each lane finding its candidate's run
+// by a search over the lanes' prefix sums, so a crowded cell does not hold the wave up.
+template <bool STAGED>
+__device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, int lane) {
+    constexpr int R = 5;
+    const uint32_t NG = a.G;
+    uint32_t hits = 0;
+    for (uint32_t base = 0; base < NG; base += kWave) {
+        const uint32_t i = base + (uint32_t)lane;
+        const bool mine = i < NG;
+        uint32_t ga = 0, rs[R], rl[R];
+        uint32_t tgt[2 * R] = {};
+        uint32_t key_i = mine ? s.hkey[i] : 0u;
+        ga = key_i & 0x3FFFu;
+        const uint32_t c = key_i >> 14;
+        const uint32_t x = c & 63u, y = (c >> 6) & 63u, z = c >> 12;
+        const uint32_t xlo = x > 0u ? x - 1u : 0u, xhi1 = (x < 63u ? x + 1u : 63u) + 1u;
+        // Targets (first cell of a run, first cell past it); an empty run has equal targets.
+        tgt[0] = 0u; tgt[1] = x < 63u ? c + 2u : c + 1u;
+        if (y < 63u) { const uint32_t row = (y + 1u) * 64u + z * 4096u; tgt[2] = row + xlo; tgt[3] = row + xhi1; }
+#pragma unroll
+        for (uint32_t k = 0; k < 3; ++k) {
+            const uint32_t yy = y + k;  // y - 1 + k, offset by one
+            if (z < 63u && yy >= 1u && yy <= 64u) {
+                const uint32_t row = (yy - 1u) * 64u + (z + 1u) * 4096u;
+                tgt[4 + 2 * k] = row + xlo; tgt[5 + 2 * k] = row + xhi1;
+            }
+        }
+        // Interleaved lower bounds over [i + 1, NG): the first position whose cell >= target.
+        uint32_t lo[2 * R], hi[2 * R];
+#pragma unroll
+        for (int k = 0; k < 2 * R; ++k) { lo[k] = mine ? i + 1u : NG; hi[k] = NG; }
+        for (uint32_t span = NG; span > 0u; span >>= 1) {
+#pragma unroll
+            for (int k = 1; k < 2 * R; ++k) {
+                if (lo[k] < hi[k]) {
+                    const uint32_t mid = (lo[k] + hi[k]) >> 1;
+                    if ((s.hkey[mid] >> 14) < tgt[k]) lo[k] = mid + 1u; else hi[k] = mid;
+                }
+            }
+        }
+        // Run 0 starts right after i; the others between their two bounds.
+        rs[0] = mine ? i + 1u : NG;
+        rl[0] = lo[1] - rs[0];
+#pragma unroll
+        for (int k = 1; k < R; ++k) { rs[k] = lo[2 * k]; rl[k] = lo[2 * k + 1] - lo[2 * k]; }
+        uint32_t n = 0;
+#pragma unroll
+        for (int k = 0; k < R; ++k) n += rl[k];
+        // Inclusive prefix over the wave's lanes; T candidates this round.
+        uint32_t inc = n;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t t = (uint32_t)__shfl_up((int)inc, d);
+            if (lane >= d) inc += t;
+        }
+        const uint32_t T = (uint32_t)__shfl((int)inc, kWave - 1);
+        const float4 pa4 = mine ? hash_geom_pos<STAGED>(md, s, ga) : make_float4(0, 0, 0, 0);
+        const uint4 ma = mine ? hash_geom_meta<STAGED>(md, hmeta, ga) : make_uint4(0, 0, 0, 0);
+        auto test = [&](const float4 pa, uint32_t body_a, uint32_t type_a, uint32_t mask_a, uint32_t group_a, uint32_t pos) {
+            const uint32_t o = s.hkey[pos] & 0x3FFFu;
+            const uint4 mb = hash_geom_meta<STAGED>(md, hmeta, o);
+            bool hit = mb.x != body_a && !((group_a & mb.z) == 0 && (mb.w & mask_a) == 0);
+            if (hit && !(type_a == GEOM_PLANE || mb.y == GEOM_PLANE)) {
+                const float4 pb4 = hash_geom_pos<STAGED>(md, s, o);
+                const f3 diff = sub(xyz(pb4), xyz(pa));
+                const float min_dist = pa.w + pb4.w + 0.1f;
+                hit = !(dot(diff, diff) >= min_dist * min_dist);
+            }
+            return hit ? 1u : 0u;
+        };
+        // Balanced rounds (no lane with more than twice the mean's chunks) walk each lane's own
+        // runs; others deal the candidates out.
+        uint32_t nmax = n;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t t = (uint32_t)__shfl_xor((int)nmax, d);
+            nmax = t > nmax ? t : nmax;
+        }
+        if (nmax <= 2u * ((T + kWave - 1u) / kWave)) {
+            uint32_t k = 0, left = rl[0], pos = rs[0];
+            for (uint32_t q = 0; q < nmax; ++q) {
+                if (q < n) {
+                    while (left == 0u) {
+                        ++k;
+                        left = k == 1 ? rl[1] : k == 2 ? rl[2] : k == 3 ? rl[3] : rl[4];
+                        pos = k == 1 ? rs[1] : k == 2 ? rs[2] : k == 3 ? rs[3] : rs[4];
+                    }
+                    hits += test(pa4, ma.x, ma.y, ma.z, ma.w, pos);
+                    ++pos;
+                    --left;
+                }
+            }
+            continue;
+        }
+        for (uint32_t t0 = 0; t0 < T; t0 += kWave) {
+            const uint32_t t = t0 + (uint32_t)lane;
+            // Owner: the first lane whose inclusive prefix exceeds t.
+            uint32_t olo = 0, ohi = kWave - 1;
+            for (int step = 0; step < 6; ++step) {
+                const uint32_t mid = (olo + ohi) >> 1;
+                const uint32_t v = (uint32_t)__shfl((int)inc, (int)mid);
+                if (v > t) ohi = mid; else olo = mid + 1u;
+            }
+            const int ow = (int)olo;
+            uint32_t u = t - ((uint32_t)__shfl((int)inc, ow) - (uint32_t)__shfl((int)n, ow));
+            uint32_t pos = 0;
+            bool found = false;
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const uint32_t len = (uint32_t)__shfl((int)rl[k], ow);
+                const uint32_t st = (uint32_t)__shfl((int)rs[k], ow);
+                if (!found && u < len) { pos = st + u; found = true; }
+                if (!found) u -= len;
+            }
+            const float4 pa = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
+            const uint32_t body_a = (uint32_t)__shfl((int)ma.x, ow), type_a = (uint32_t)__shfl((int)ma.y, ow);
+            const uint32_t mask_a = (uint32_t)__shfl((int)ma.z, ow), group_a = (uint32_t)__shfl((int)ma.w, ow);
+            if (t < T && found) hits += test(pa, body_a, type_a, mask_a, group_a, pos);
+        }
+    }
+    for (int d = 1; d < kWave; d <<= 1) hits += (uint32_t)__shfl_xor((int)hits, d);
     return hits;
 }
 
@@ -1236,7 +1368,13 @@ void step_kernel(StepArgs a) {
                 }
             }
             // Queries (broad_phase_detect, :632-700): count each geom's pairs, place them
-            // with a prefix sum over the env's lanes, then write them.
+            // with a prefix sum over the env's lanes, then write them. A full list whose
+            // count cannot wrap past 2^32 this substep (at most G (G - 1) / 2 pairs) takes
+            // no append, so only the number of pairs is needed.
+            const uint64_t max_pairs = (uint64_t)a.G * (uint64_t)(a.G - 1u) / 2u;
+            if (live && count >= M && (uint64_t)count + max_pairs <= 0xFFFFFFFFull) {
+                count += hash_count_forward<HBM>(a, md, s, hmeta, sl);
+            } else
             for (uint32_t base = 0; base < a.G; base += G) {
                 const uint32_t g = base + sl;
                 const bool mine = live && g < a.G;
