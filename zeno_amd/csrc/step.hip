@@ -838,15 +838,8 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
             }
             continue;
         }
-        for (uint32_t t0 = 0; t0 < T; t0 += kWave) {
-            const uint32_t t = t0 + (uint32_t)lane;
-            // Owner: the first lane whose inclusive prefix exceeds t.
-            uint32_t olo = 0, ohi = kWave - 1;
-            for (int step = 0; step < 6; ++step) {
-                const uint32_t mid = (olo + ohi) >> 1;
-                const uint32_t v = (uint32_t)__shfl((int)inc, (int)mid);
-                if (v > t) ohi = mid; else olo = mid + 1u;
-            }
+        // Two candidates per lane and trip (t and t + 64), their searches side by side.
+        auto deal = [&](uint32_t t, uint32_t olo) {
             const int ow = (int)olo;
             uint32_t u = t - ((uint32_t)__shfl((int)inc, ow) - (uint32_t)__shfl((int)n, ow));
             uint32_t pos = 0;
@@ -858,10 +851,30 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
                 if (!found && u < len) { pos = st + u; found = true; }
                 if (!found) u -= len;
             }
-            const float4 pa = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
-            const uint32_t body_a = (uint32_t)__shfl((int)ma.x, ow), type_a = (uint32_t)__shfl((int)ma.y, ow);
-            const uint32_t mask_a = (uint32_t)__shfl((int)ma.z, ow), group_a = (uint32_t)__shfl((int)ma.w, ow);
-            if (t < T && found) hits += test(pa, body_a, type_a, mask_a, group_a, pos);
+            float4 pa;
+            uint4 mo;
+            if (STAGED) {  // the owner's geom from the staged arrays
+                const uint32_t go = (uint32_t)__shfl((int)ga, ow);
+                pa = hash_geom_pos<STAGED>(md, s, go);
+                mo = hash_geom_meta<STAGED>(md, hmeta, go);
+            } else {
+                pa = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
+                mo = make_uint4((uint32_t)__shfl((int)ma.x, ow), (uint32_t)__shfl((int)ma.y, ow),
+                                (uint32_t)__shfl((int)ma.z, ow), (uint32_t)__shfl((int)ma.w, ow));
+            }
+            return (t < T && found) ? test(pa, mo.x, mo.y, mo.z, mo.w, pos) : 0u;
+        };
+        for (uint32_t t0 = 0; t0 < T; t0 += 2u * kWave) {
+            const uint32_t tA = t0 + (uint32_t)lane, tB = tA + kWave;
+            // Owners: the first lane whose inclusive prefix exceeds t.
+            uint32_t loA = 0, hiA = kWave - 1, loB = 0, hiB = kWave - 1;
+            for (int step = 0; step < 6; ++step) {
+                const uint32_t midA = (loA + hiA) >> 1, midB = (loB + hiB) >> 1;
+                const uint32_t vA = (uint32_t)__shfl((int)inc, (int)midA), vB = (uint32_t)__shfl((int)inc, (int)midB);
+                if (vA > tA) hiA = midA; else loA = midA + 1u;
+                if (vB > tB) hiB = midB; else loB = midB + 1u;
+            }
+            hits += deal(tA, loA) + deal(tB, loB);
         }
     }
     for (int d = 1; d < kWave; d <<= 1) hits += (uint32_t)__shfl_xor((int)hits, d);
