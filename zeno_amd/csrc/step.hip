@@ -999,9 +999,9 @@ void step_kernel(StepArgs a) {
     Slot4 c0{}, c1{}, c2{}, c3{};
     if (live && do_solve) {
         if (b0 < B && !alias) {
-            p_vel = a.vel[eb + b0];
             p_pos = a.pos[eb + b0];
             p_quat = a.quat[eb + b0];
+            p_vel = a.vel[eb + b0];
             p_ang = a.angvel[eb + b0];
         }
         if (PRE2 && b0 + G < B) {
@@ -1200,16 +1200,17 @@ void step_kernel(StepArgs a) {
         // (every |tau| < 1e-6, so stage C adds nothing), each body's forces feed its own
         // integration at once, in registers (the same operations as B then D), and the force,
         // torque and contribution arrays are neither written nor read.
-        bool fuse = false;
-        if (HBM) {
+        auto joint_forces_absent = [&]() {
             wave_sync<HBM>();  // the torques apply_actions wrote
             bool contrib = false;
             if (live && do_solve) {
                 for (uint32_t j = sl; j < a.J; j += G) contrib = contrib || !(__builtin_fabsf(s.jt[j]) < 1e-6f);
             }
-            fuse = __ballot(contrib) == 0ull;
-        }
-        if (HBM && live && do_solve && fuse) {
+            return __ballot(contrib) == 0ull;
+        };
+        const bool fuse = HBM ? joint_forces_absent() : false;
+        if constexpr (HBM) {
+        if (live && do_solve && fuse) {
             if (bf != 0u && sl == 0) {
                 s.ppos[0] = s.pos[0];
                 s.pquat[0] = s.quat[0];
@@ -1254,7 +1255,8 @@ void step_kernel(StepArgs a) {
                 s.quat[b] = tof4(q);
             }
         }
-        if (HBM && live && do_solve && !fuse) stage_b();
+        if (live && do_solve && !fuse) stage_b();
+        }
         wave_sync<HBM>();
         // ---- C: apply_joint_forces (S2, :122-190) -------------------------------------
         // Each joint's world-frame contribution axis_world * tau is formed by one lane into
@@ -2058,17 +2060,16 @@ void step_kernel(StepArgs a) {
                 float jp = 0.0f, jv = 0.0f;
                 // Working sets in HBM: the orientations are read only by the joint types that
                 // use them.
-                q4 q_a = mk4(0.0f, 0.0f, 0.0f, 1.0f), q_b = q_a;
-                if (!HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
+                const bool uses_q = !HBM || type == JOINT_REVOLUTE || type == JOINT_PRISMATIC;
+                const q4 q_a = uses_q ? toq(s.quat[ja]) : mk4(0.0f, 0.0f, 0.0f, 1.0f);
+                const q4 q_b = uses_q ? toq(s.quat[jb]) : mk4(0.0f, 0.0f, 0.0f, 1.0f);
                 if (type == JOINT_REVOLUTE) {
-                    if (HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
                     const f3 axis_local = mk3(jr.axis[0], jr.axis[1], jr.axis[2]);
                     const f3 aw = qrot(axis_local, q_a);
                     const q4 q_rel = qmul(qconj(q_a), q_b);
                     jp = 2.0f * z_atan2f(dot(xyz(q_rel), axis_local), q_rel.w);
                     jv = dot(sub(xyz(s.angvel[jb]), xyz(s.angvel[ja])), aw);
                 } else if (type == JOINT_PRISMATIC) {
-                    if (HBM) { q_a = toq(s.quat[ja]); q_b = toq(s.quat[jb]); }
                     const f3 aw = qrot(mk3(jr.axis[0], jr.axis[1], jr.axis[2]), q_a);
                     const f3 r_a = qrot(mk3(jr.anchor_parent[0], jr.anchor_parent[1], jr.anchor_parent[2]), q_a);
                     const f3 r_b = qrot(mk3(jr.anchor_child[0], jr.anchor_child[1], jr.anchor_child[2]), q_b);
