@@ -159,3 +159,31 @@ def test_hash_count_only_matches_oracle():
         compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
     assert np.all(o.contact_counts[1:3] >= 16)
     g.close()
+
+
+@pytest.mark.parametrize("substeps", [1, 2])
+def test_bodies_finished_at_integration_match_oracle(substeps):
+    """Working sets in HBM with a full list: the bodies no slot or constraint names are finished
+    by the fused integration (velocity update and accelerations in registers, no previous pose
+    stored); the others take the velocity update. The hash pile forced into placement 2 with a
+    16-slot list: without views, with the body views held (the write-back then writes every
+    acceleration), and through step_subset, every step against the oracle."""
+    g, o, acts = make_pair("pile_hash", 3, 9, seed=17, max_contacts=16, placement=2, substeps=substeps)
+    assert g.modes()["placement"] == 2
+    for k in range(3):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    held = (g.get_body_positions(zero_copy=True), g.get_body_velocities(zero_copy=True))
+    for k in range(3, 6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+        np.testing.assert_array_equal(held[0], g.get_body_positions(zero_copy=False))
+    mask = np.array([1, 0, 1], np.uint8)
+    for k in range(6, 9):
+        g.step_subset(acts[k], mask)
+        o.step_subset(acts[k], mask)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+    assert np.all(o.contact_counts >= 16)
+    g.close()

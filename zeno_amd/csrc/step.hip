@@ -1200,6 +1200,36 @@ void step_kernel(StepArgs a) {
         // (every |tau| < 1e-6, so stage C adds nothing), each body's forces feed its own
         // integration at once, in registers (the same operations as B then D), and the force,
         // torque and contribution arrays are neither written nor read.
+        // A full list that this substep cannot wrap takes no append (see the count-only broad
+        // phase), so the bodies its slots name are known before the broad phase runs. A dynamic,
+        // non-kinematic body that no constraint template and no slot names is moved by nothing
+        // between integration and the velocity update: with the working sets in HBM, the fused
+        // integration finishes it (the update's velocities from the same operands, and the
+        // last substep's accelerations), and the velocity update skips it (the lane keeps one
+        // bit per body of its loop), so its previous pose is neither written nor read.
+        const uint64_t max_appends = HASH ? (uint64_t)a.G * (uint64_t)(a.G - 1u) / 2u : (uint64_t)a.P;
+        const uint32_t named_cap = PL == PL_ALL_HBM ? a.lds_small.ppen - a.lds_small.skey : a.lds.ppen - a.lds.skey;
+        const bool frozen = HBM && live && count >= M && (uint64_t)count + max_appends <= 0xFFFFFFFFull &&
+                            B <= bf + 32u * (uint32_t)G && B <= named_cap;
+        uint32_t early_bits = 0;  // bit k: this lane's k-th body of the per-body loops finished early
+        // One byte per body on the sort-key region (dead until the broad phase); the slots' lanes
+        // store 1 for both of their bodies (equal stores, no atomics). The region is in LDS but
+        // for placement 3, so a wave-level fence orders it there.
+        uint8_t* const named = (uint8_t*)s.skey;
+        auto mark_named = [&]() {
+            const uint32_t words = (B + 3u) / 4u;
+            for (uint32_t w = sl; w < words; w += G) ((uint32_t*)named)[w] = 0u;
+            wave_sync<PL == PL_WORK_HBM>();
+            for (uint32_t k = sl; k < M; k += G) {
+                const uint32_t* idx = s.con[s.perm[k]].indices;
+                named[idx[0]] = 1u;
+                named[idx[1]] = 1u;
+            }
+            wave_sync<PL == PL_WORK_HBM>();
+        };
+        auto finished_early = [&](uint32_t b, float4 imi) {
+            return frozen && !(imi.x < 1e-8f) && (md.flags[b] & 5u) == 0u && named[b] == 0u;
+        };
         auto joint_forces_absent = [&]() {
             wave_sync<HBM>();  // the torques apply_actions wrote
             bool contrib = false;
@@ -1210,13 +1240,16 @@ void step_kernel(StepArgs a) {
         };
         const bool fuse = HBM ? joint_forces_absent() : false;
         if constexpr (HBM) {
+        if (frozen && fuse && do_solve) mark_named();
         if (live && do_solve && fuse) {
+            const float inv_dt = 1.0f / a.dt;
             if (bf != 0u && sl == 0) {
                 s.ppos[0] = s.pos[0];
                 s.pquat[0] = s.quat[0];
                 if (take_vb) s.vb[0] = s.vel[0];
             }
-            for (uint32_t b = bf + sl; b < B; b += G) {
+            uint32_t kb = 0;
+            for (uint32_t b = bf + sl; b < B; b += G, ++kb) {
                 const float4 imi = md.invmi[b];
                 float4 P = s.pos[b], Q = s.quat[b];
                 const float4 V = s.vel[b];
@@ -1237,13 +1270,15 @@ void step_kernel(StepArgs a) {
                     s.pos[b] = P;
                     s.quat[b] = Q;
                 }
-                s.ppos[b] = P;
-                s.pquat[b] = Q;
+                const bool early = finished_early(b, imi);
+                if (!early) {
+                    s.ppos[b] = P;
+                    s.pquat[b] = Q;
+                }
                 if (!dyn) continue;
                 f3 vel = add(xyz(V), scale(scale(force, imi.x), a.dt));
                 vel = scale(vel, 0.999f);
                 f3 pos = add(xyz(P), scale(vel, a.dt));
-                s.vel[b] = tof4(vel, 0.0f);
                 s.pos[b] = tof4(pos, 0.0f);
                 f3 om = add(xyz(s.angvel[b]), scale(mul(mk3(imi.y, imi.z, imi.w), torque), a.dt));
                 om = scale(om, 0.999f);
@@ -1251,8 +1286,23 @@ void step_kernel(StepArgs a) {
                 f3 h = scale(scale(om, a.dt), 0.5f);
                 q = qadd(q, qmul(mk4(h.x, h.y, h.z, 0.0f), q));
                 q = qnormalize(q);
-                s.angvel[b] = tof4(om, 0.0f);
                 s.quat[b] = tof4(q);
+                if (!early) {
+                    s.vel[b] = tof4(vel, 0.0f);
+                    s.angvel[b] = tof4(om, 0.0f);
+                    continue;
+                }
+                // The velocity update's values (pose now minus previous pose), from registers.
+                early_bits |= 1u << kb;
+                const float4 v = tof4(scale(sub(pos, xyz(P)), inv_dt), 0.0f);
+                s.vel[b] = v;
+                q4 dq = qmul(toq(tof4(q)), qconj(toq(Q)));
+                if (dq.w < 0) dq = qneg(dq);
+                s.angvel[b] = tof4(scale(sscale(2.0f, xyz(dq)), inv_dt), 0.0f);
+                if (j_acc && step + 1 == a.substeps) {
+                    const float4 v0 = take_vb ? V : s.vb[b];
+                    a.acc[(size_t)env * B + b] = make_float4((v.x - v0.x) * a.inv_step, (v.y - v0.y) * a.inv_step, (v.z - v0.z) * a.inv_step, 0.0f);
+                }
             }
         }
         if (live && do_solve && !fuse) stage_b();
@@ -2037,7 +2087,9 @@ void step_kernel(StepArgs a) {
         if (live && do_solve) {
             const float inv_dt = 1.0f / a.dt;
             const bool acc_here = j_acc && step + 1 == a.substeps;
-            for (uint32_t b = bf + sl; b < B; b += G) {
+            uint32_t kb = 0;
+            for (uint32_t b = bf + sl; b < B; b += G, ++kb) {
+                if (HBM && ((early_bits >> kb) & 1u) != 0u) continue;
                 if (md.invmi[b].x < 1e-8f) continue;
                 const float4 v = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
                 s.vel[b] = v;

@@ -162,6 +162,11 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         com[b] = make_float4(m.bodies[b].com_offset[0], m.bodies[b].com_offset[1], m.bodies[b].com_offset[2], 0.0f);
         flags[b] = ((uint32_t)m.bodies[b].params[1] == 1u ? 1u : 0u) | (im[0] > 1e-8f ? 2u : 0u);
     }
+    // Bit 2: the body takes part in a constraint template (a joint solve may move it).
+    for (const ConstraintRec& t : m.templates) {
+        if (t.indices[0] < w->B) flags[t.indices[0]] |= 4u;
+        if (t.indices[1] < w->B) flags[t.indices[1]] |= 4u;
+    }
     w->b0_static = w->B > 1 && invmi[0].x < 1e-8f && (flags[0] & 1u) == 0u;
     std::vector<float4> jrec;
     std::vector<JointPhase> jph;
