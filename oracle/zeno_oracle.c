@@ -6,7 +6,43 @@
  * single environment, in the order World.stepOnce dispatches them
  * (src/world/world.zig:934-1293). Build with -ffp-contract=off and without fast-math.
  *
- * Parity status of each function (how it is pinned) is listed in tests/test_oracle.py.
+ * How each function is pinned (tests/, by checks that do not restate its code; every
+ * function is pinned, none is left "parity unpinned"):
+ *   zo_atan2f, zo_asinf        float64 ground truth within 3 ulp, IEEE special cases
+ *                              (test_oracle.py)
+ *   k_apply_actions            the reference's actuator KATs, clamp order (test_oracle.py,
+ *                              test_oracle_pins.py)
+ *   k_compute_forces           gravity torque (R c) x m g on an offset-COM body (test_oracle_pins.py)
+ *   k_update_kinematic         closed form of a kinematic body (test_oracle.py)
+ *   k_apply_joint_forces       motors on hinges and slides, parent reaction, 1e-6 threshold
+ *                              (test_oracle.py, test_oracle_pins.py)
+ *   k_save_prev, k_integrate   free-body closed form, world-frame angular velocity, order and
+ *                              renormalisation (test_oracle.py, test_oracle_pins.py)
+ *   k_broad_phase              fixtures C1-C3, margin, contype/conaffinity rule, plane rule
+ *                              (test_oracle.py, test_oracle_pins.py, test_count_wrap.py)
+ *   k_broad_phase_hash         cell closed forms, the pair set and order, threshold, filters,
+ *                              overflow (test_hash.py)
+ *   k_sort_contacts            stable sort by (min<<16)|max, wraps (test_oracle.py, test_count_wrap.py)
+ *   k_narrow_phase             reference KATs, capsule endpoint, overlap midpoint, friction
+ *                              mean, plane height (test_oracle.py, test_oracle_pins.py)
+ *   k_match_cached             hand-built cases: radius, nearest, ties (test_oracle.py)
+ *   k_solve_joints             closed forms per constraint type, COM levers, targets, limits
+ *                              (test_oracle.py, test_oracle_pins.py)
+ *   k_solve_contacts           physical laws of one contact step, restitution, correction
+ *                              split (test_contact_solve.py, test_oracle_pins.py)
+ *   k_warm_start, k_store_lambda   the 0.8 factor and the stored lambda (test_contact_solve.py,
+ *                              test_oracle_pins.py)
+ *   k_update_velocities        shortest-arc angular velocity (test_oracle_pins.py)
+ *   k_update_joint_states      hinge and slide states (test_oracle.py, test_oracle_pins.py)
+ *   k_read_sensors             frame, accelerometer and gyro sensors (test_oracle.py,
+ *                              test_oracle_pins.py, test_contact_solve.py)
+ *   k_cache_contacts, zo_step  snapshot, substep dt, accelerations (test_oracle_pins.py)
+ *   zo_collide_env             extended-contact slots (test_ext_contacts.py)
+ *   zo_build_templates         fixtures C1-C4, template fields per joint type, colouring
+ *                              (test_oracle.py, test_model.py)
+ *   zo_detect_collision(s)     float64 geometry per pair, dispatch flips (test_narrow_ext.py)
+ * tests/test_oracle_mutants.py plants plausible misreadings of the reference in a copy of
+ * this file; each must fail at least one of those pins.
  *
  * Where the reference runs unordered atomics or races, this oracle fixes one sequential
  * schedule (the HIP kernel reproduces the same):
