@@ -43,19 +43,25 @@ def masked_scene(nbodies: int, two_geoms_every: int, seed: int) -> str:
     return "\n".join(lines)
 
 
-def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M, epw: int = 1):
-    saved = os.environ.get("ZENO_AMD_ENVS_PER_WAVE")
-    os.environ["ZENO_AMD_ENVS_PER_WAVE"] = str(epw)
+def pair_one_env_per_wave(xml: str, envs: int, max_contacts: int = M, epw: int = 1, split: bool = None):
+    overrides = {"ZENO_AMD_ENVS_PER_WAVE": str(epw), "ZENO_AMD_SPLIT": None if split is None else str(int(split))}
+    saved = {k: os.environ.get(k) for k in overrides}
     try:
+        for k, v in overrides.items():
+            if v is not None:
+                os.environ[k] = v
         g = ZenoWorld(mjcf_string=xml, num_envs=envs, max_contacts_per_env=max_contacts)
     finally:
-        if saved is None:
-            os.environ.pop("ZENO_AMD_ENVS_PER_WAVE")
-        else:
-            os.environ["ZENO_AMD_ENVS_PER_WAVE"] = saved
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     m = load_model(mjcf_string=xml)
     o = OracleWorld(m, envs, max_contacts_per_env=max_contacts)
     assert g.launch_config()[0] == epw
+    if split is not None:
+        assert g.split_groups() == split
     return m, g, o
 
 
@@ -72,12 +78,12 @@ def hinged_row(n: int) -> str:
 @pytest.mark.parametrize("scene,epw", [("free32", 2), ("free16", 4), ("hinged16", 4), ("hinged64", 1)])
 def test_static_world_body_set_aside(scene, epw):
     """Scenes whose bodies after the world body fill whole passes of an environment's lanes
-    (B - 1 = 64 / EPW or 64): the per-body stages take bodies 1.. across the lanes and set the
-    static world body aside. Free bodies, and bodies hinged to the world (whose joints read
+    (B - 1 = 64 / EPW or 64), without split groups: the per-body stages take bodies 1.. across
+    the lanes and set the static world body aside. Free bodies, and bodies hinged to the world (whose joints read
     the world body's pose), every step against the oracle."""
     xml = {"free32": masked_scene(32, 1000, 7), "free16": masked_scene(16, 1000, 8),
            "hinged16": hinged_row(16), "hinged64": hinged_row(64)}[scene]
-    m, g, o = pair_one_env_per_wave(xml, 8, max_contacts=16, epw=epw)
+    m, g, o = pair_one_env_per_wave(xml, 8, max_contacts=16, epw=epw, split=False)
     assert (m["num_bodies"] - 1) % (64 // epw) == 0
     for _ in range(12):
         g.step(np.zeros((8, 0), np.float32))
