@@ -193,3 +193,34 @@ def test_bodies_finished_at_integration_match_oracle(substeps):
         compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
     assert np.all(o.contact_counts >= 16)
     g.close()
+
+
+@pytest.mark.parametrize("region", ["upper", "mixed"])
+def test_hash_count_only_at_the_grid_edges(region):
+    """Count-only hash queries where the runs meet the grid's edges: bodies around cells 62-63
+    on every axis (coordinates up to 66 clamp into cell 63, so x + 1, y + 1 and z + 1 leave
+    the grid), and a mixed layout of the far corner, the origin's clamped cells and open
+    space, every step against the oracle with a 16-slot list."""
+    g, o, acts = make_pair("pile_hash", 3, 6, seed=23, max_contacts=16)
+    state = [o.positions.copy(), o.quaternions.copy(), o.velocities.copy(), o.angular_velocities.copy()]
+    rng = np.random.default_rng(29)
+    n = o.B - 1
+    if region == "upper":
+        state[0][:, 1:, :3] = rng.uniform(61.5, 66.0, (3, n, 3)).astype(np.float32)
+    else:
+        pick = rng.integers(0, 3, n)
+        far = rng.uniform(61.5, 66.0, (3, n, 3))
+        low = rng.uniform(-3.0, 1.5, (3, n, 3))
+        mid = rng.uniform(10.0, 14.0, (3, n, 3))
+        state[0][:, 1:, :3] = np.where(pick[None, :, None] == 0, far, np.where(pick[None, :, None] == 1, low, mid)).astype(np.float32)
+    state[2][:] = 0.0
+    state[3][:] = 0.0
+    g.reset_to_state(*state)
+    o.reset_to_state(*state)
+    for k in range(6):
+        g.step(acts[k])
+        o.step(acts[k])
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+        np.testing.assert_array_equal(g.get_cell_ids(), o.cell_ids[:, : g.num_geoms])
+    assert np.all(o.contact_counts >= 16)
+    g.close()
