@@ -359,3 +359,28 @@ def test_device_resident_loop_matches_host_loop():
         compare(gpu_arrays(g1), gpu_arrays(g2), rtol=0, atol=0)
     finally:
         hip.hipFree(dptr)
+
+
+def test_worlds_side_by_side_stay_independent():
+    """Several worlds in one process (a training and an evaluation batch, say): Ant, the
+    pendulum and the pile stepped in turn, with the first world's observation view held (its
+    steps are synchronous, the others' are not), each against its own oracle; the pendulum is
+    closed halfway and the other two go on."""
+    worlds = [make_pair("ant", 48, 12, seed=51), make_pair("pendulum", 20, 12, seed=52), make_pair("pile", 6, 12, seed=53)]
+    held = worlds[0][0].get_observations(zero_copy=True)
+    for k in range(12):
+        for i, (g, o, acts) in enumerate(worlds):
+            if g is None:
+                continue
+            g.step(acts[k])
+            o.step(acts[k] if o.A else None)
+        np.testing.assert_array_equal(held, worlds[0][1].observations[:, : worlds[0][1].model["obs_dim"]])
+        for g, o, _ in worlds:
+            if g is not None:
+                compare(gpu_arrays(g), oracle_arrays(o), **TOL)
+        if k == 5:
+            worlds[1][0].close()
+            worlds[1] = (None, None, None)
+    for g, _, _ in worlds:
+        if g is not None:
+            g.close()
