@@ -53,3 +53,36 @@ def test_cell_ids_need_the_hash():
     assert g.modes()["spatial_hash"] is False
     with pytest.raises(RuntimeError):
         g.get_cell_ids()
+
+
+@pytest.mark.parametrize("num_bodies", [512, 1023, 1024, 1500])
+def test_hash_key_sort_sizes(num_bodies):
+    """The sort of the hash keys at the sizes that change its form: 513 geoms (the smallest
+    scene hashed, padded to 1024 keys), 1024 (every one of the 1024 places a real key), 1025
+    (padded to 2048: the network runs in LDS instead of registers) and 1501. Piles of that
+    many bodies at the 601-body pile's density, every step against the oracle, cell ids
+    included."""
+    import os
+    from oracle.oracle import OracleWorld
+    from zeno_amd.model import load_model
+    from zeno_amd.scenes import pile_initial_state, pile_mjcf
+    from zeno_amd.world import ZenoWorld
+    side = 16.0 * np.sqrt(num_bodies / 600.0)
+    xy = (-3.0, -3.0 + side)
+    xml = pile_mjcf(num_bodies, seed=num_bodies, xy=xy)
+    m = load_model(mjcf_string=xml)
+    assert m["num_geoms"] == num_bodies + 1
+    g = ZenoWorld(mjcf_string=xml, num_envs=3)
+    o = OracleWorld(m, 3)
+    assert g.modes()["spatial_hash"]
+    state = pile_initial_state(m, 3, num_bodies + 1, xy=xy)
+    g.reset_to_state(*state)
+    o.reset_to_state(*state)
+    G = m["num_geoms"]
+    for k in range(5):
+        g.step(np.zeros((3, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), rtol=1e-4, atol=1e-4)
+        np.testing.assert_array_equal(g.get_cell_ids(), o.cell_ids[:, :G], err_msg=f"cell ids, step {k}")
+    assert (o.contact_counts > 0).all()
+    g.close()

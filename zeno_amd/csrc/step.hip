@@ -663,6 +663,49 @@ __device__ __forceinline__ uint32_t hash_axis(float p) {
     return !(f >= 0.0f) ? 0u : (f >= 63.0f ? 63u : (uint32_t)f);
 }
 
+// Bitonic sort of n <= 1024 keys held in registers, one wave: lane l holds elements
+// 16 l .. 16 l + 15 (positions from n on read as 0xFFFFFFFF and sort last, so the first n
+// sorted elements are the n keys sorted). Passes whose partners are less than 16 apart
+// compare registers of one lane; the others pair lane l with lane l ^ (distance / 16), each
+// lane keeping the smaller or the larger of its two values. A sorting network's output is the
+// sorted sequence whatever its steps, so the keys come out as any sort leaves them.
+__device__ __forceinline__ void sort_keys_1024(uint32_t* key, uint32_t n, uint32_t lane) {
+    uint32_t v[16];
+#pragma unroll
+    for (uint32_t r = 0; r < 16; ++r) v[r] = 16u * lane + r < n ? key[16u * lane + r] : 0xFFFFFFFFu;
+#pragma unroll
+    for (uint32_t k = 2; k <= 1024; k <<= 1) {
+#pragma unroll
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            if (j >= 16) {
+                const int d = (int)(j >> 4);
+                const bool lower = (lane & (uint32_t)d) == 0u;
+                const bool asc = ((16u * lane) & k) == 0u;
+                const bool take_min = lower == asc;
+#pragma unroll
+                for (uint32_t r = 0; r < 16; ++r) {
+                    const uint32_t p = (uint32_t)__shfl_xor((int)v[r], d);
+                    v[r] = take_min ? (v[r] < p ? v[r] : p) : (v[r] < p ? p : v[r]);
+                }
+            } else {
+#pragma unroll
+                for (uint32_t r = 0; r < 16; ++r) {
+                    if ((r & j) != 0u) continue;
+                    const uint32_t r2 = r | j;
+                    const bool asc = k < 16 ? (r & k) == 0u : ((16u * lane) & k) == 0u;
+                    const uint32_t lo = v[r] < v[r2] ? v[r] : v[r2], hi = v[r] < v[r2] ? v[r2] : v[r];
+                    v[r] = asc ? lo : hi;
+                    v[r2] = asc ? hi : lo;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < 16; ++r) {
+        if (16u * lane + r < n) key[16u * lane + r] = v[r];
+    }
+}
+
 // First position in key[lo, n) whose cell is >= cell.
 __device__ __forceinline__ uint32_t hash_lower_bound(const uint32_t* key, uint32_t lo, uint32_t n, uint32_t cell) {
     uint32_t hi = n;
@@ -1418,7 +1461,12 @@ void step_kernel(StepArgs a) {
                 }
             }
             wave_sync<HBM>();
-            // Bitonic sort of the Gp keys: one compare-exchange pair per lane and pass.
+            // Bitonic sort of the Gp keys: up to 1024 in registers (sixteen per lane), more in
+            // LDS, one compare-exchange pair per lane and pass.
+            if (a.Gp <= 1024u) {
+                if (live) sort_keys_1024(s.hkey, a.Gp, (uint32_t)sl);
+                wave_sync<HBM>();
+            } else
             for (uint32_t k = 2; k <= a.Gp; k <<= 1) {
                 for (uint32_t j = k >> 1; j > 0; j >>= 1) {
                     if (live) {
