@@ -706,16 +706,6 @@ __device__ __forceinline__ void sort_keys_1024(uint32_t* key, uint32_t n, uint32
     }
 }
 
-// First position in key[lo, n) whose cell is >= cell.
-__device__ __forceinline__ uint32_t hash_lower_bound(const uint32_t* key, uint32_t lo, uint32_t n, uint32_t cell) {
-    uint32_t hi = n;
-    while (lo < hi) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if ((key[mid] >> 14) < cell) lo = mid + 1; else hi = mid;
-    }
-    return lo;
-}
-
 // Pairs (g, other > g) of one geom (:632-700). Returns their number; with emit set, writes
 // pair k to logical slot `slot + k` while that is below M.
 // STAGED: the geom data come from hpos / hmeta (working sets in HBM); otherwise from the
@@ -744,6 +734,34 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
     const uint32_t id = s.hcell[g];
     const int cx = (int)(id & 63u), cy = (int)((id >> 6) & 63u), cz = (int)(id >> 12);
     const uint32_t xlo = cx > 0 ? (uint32_t)cx - 1u : 0u, xhi = cx < 63 ? (uint32_t)cx + 1u : 63u;
+    // The nine rows' first positions (first key whose cell is >= the row's first cell), by
+    // binary searches run side by side: each step reads the nine midpoints unconditionally,
+    // so the reads are in flight together. Rows outside the grid keep lo = G (no keys).
+    uint32_t lo[9], hi[9], tg[9];
+#pragma unroll
+    for (int r = 0; r < 9; ++r) {
+        const int ny = cy + r % 3 - 1, nz = cz + r / 3 - 1;
+        const bool in = ny >= 0 && ny <= 63 && nz >= 0 && nz <= 63;
+        tg[r] = in ? (uint32_t)ny * 64u + (uint32_t)nz * 4096u + xlo : 0u;
+        lo[r] = in ? 0u : a.G;
+        hi[r] = a.G;
+    }
+    for (uint32_t span = a.G; span > 0u; span >>= 1) {
+        uint32_t kv[9];
+#pragma unroll
+        for (int r = 0; r < 9; ++r) {
+            const uint32_t mid = (lo[r] + hi[r]) >> 1;
+            kv[r] = s.hkey[mid < a.G ? mid : a.G - 1u];
+        }
+#pragma unroll
+        for (int r = 0; r < 9; ++r) {
+            const uint32_t mid = (lo[r] + hi[r]) >> 1;
+            const bool act = lo[r] < hi[r];
+            const bool below = (kv[r] >> 14) < tg[r];
+            lo[r] = act && below ? mid + 1u : lo[r];
+            hi[r] = act && !below ? mid : hi[r];
+        }
+    }
     uint32_t hits = 0;
     for (int dz = -1; dz <= 1; ++dz) {
         const int nz = cz + dz;
@@ -753,7 +771,10 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
             if (ny < 0 || ny > 63) continue;
             const uint32_t row = (uint32_t)ny * 64u + (uint32_t)nz * 4096u;
             const uint32_t last = (row + xhi) << 14 | 0x3FFFu;  // largest key of the row's cells
-            for (uint32_t k = hash_lower_bound(s.hkey, 0, a.G, row + xlo); k < a.G; ++k) {
+            const int r = (dz + 1) * 3 + (dy + 1);
+            const uint32_t first = r == 0 ? lo[0] : r == 1 ? lo[1] : r == 2 ? lo[2] : r == 3 ? lo[3] : r == 4 ? lo[4]
+                                 : r == 5 ? lo[5] : r == 6 ? lo[6] : r == 7 ? lo[7] : lo[8];
+            for (uint32_t k = first; k < a.G; ++k) {
                 const uint32_t key = s.hkey[k];
                 if (key > last) break;
                 const uint32_t o = key & 0x3FFFu;
@@ -820,13 +841,22 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
         uint32_t lo[2 * R], hi[2 * R];
 #pragma unroll
         for (int k = 0; k < 2 * R; ++k) { lo[k] = mine ? i + 1u : NG; hi[k] = NG; }
+        // Each step reads the nine midpoints unconditionally (a finished search reads a valid
+        // place and keeps its bounds), so the nine reads are in flight together.
         for (uint32_t span = NG; span > 0u; span >>= 1) {
+            uint32_t kv[2 * R];
 #pragma unroll
             for (int k = 1; k < 2 * R; ++k) {
-                if (lo[k] < hi[k]) {
-                    const uint32_t mid = (lo[k] + hi[k]) >> 1;
-                    if ((s.hkey[mid] >> 14) < tgt[k]) lo[k] = mid + 1u; else hi[k] = mid;
-                }
+                const uint32_t mid = (lo[k] + hi[k]) >> 1;
+                kv[k] = s.hkey[mid < NG ? mid : NG - 1u];
+            }
+#pragma unroll
+            for (int k = 1; k < 2 * R; ++k) {
+                const uint32_t mid = (lo[k] + hi[k]) >> 1;
+                const bool act = lo[k] < hi[k];
+                const bool below = (kv[k] >> 14) < tgt[k];
+                lo[k] = act && below ? mid + 1u : lo[k];
+                hi[k] = act && !below ? mid : hi[k];
             }
         }
         // Run 0 starts right after i; the others between their two bounds.
@@ -846,18 +876,6 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
         const uint32_t T = (uint32_t)__shfl((int)inc, kWave - 1);
         const float4 pa4 = mine ? hash_geom_pos<STAGED>(md, s, ga) : make_float4(0, 0, 0, 0);
         const uint4 ma = mine ? hash_geom_meta<STAGED>(md, hmeta, ga) : make_uint4(0, 0, 0, 0);
-        auto test = [&](const float4 pa, uint32_t body_a, uint32_t type_a, uint32_t mask_a, uint32_t group_a, uint32_t pos) {
-            const uint32_t o = s.hkey[pos] & 0x3FFFu;
-            const uint4 mb = hash_geom_meta<STAGED>(md, hmeta, o);
-            bool hit = mb.x != body_a && !((group_a & mb.z) == 0 && (mb.w & mask_a) == 0);
-            if (hit && !(type_a == GEOM_PLANE || mb.y == GEOM_PLANE)) {
-                const float4 pb4 = hash_geom_pos<STAGED>(md, s, o);
-                const f3 diff = sub(xyz(pb4), xyz(pa));
-                const float min_dist = pa.w + pb4.w + 0.1f;
-                hit = !(dot(diff, diff) >= min_dist * min_dist);
-            }
-            return hit ? 1u : 0u;
-        };
         // Balanced rounds (no lane with more than twice the mean's chunks) walk each lane's own
         // runs; others deal the candidates out.
         uint32_t nmax = n;
@@ -866,58 +884,116 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
             nmax = t > nmax ? t : nmax;
         }
         if (nmax <= 2u * ((T + kWave - 1u) / kWave)) {
+            // Four of the lane's candidates per trip: their positions first, then their reads
+            // side by side, then the tests of hash_pairs_of (different bodies, contype /
+            // conaffinity, and the distance unless a plane takes part; the distance is evaluated
+            // whatever the other conditions give and combined with them after).
+            constexpr int U = 4;
             uint32_t k = 0, left = rl[0], pos = rs[0];
-            for (uint32_t q = 0; q < nmax; ++q) {
-                if (q < n) {
-                    while (left == 0u) {
-                        ++k;
-                        left = k == 1 ? rl[1] : k == 2 ? rl[2] : k == 3 ? rl[3] : rl[4];
-                        pos = k == 1 ? rs[1] : k == 2 ? rs[2] : k == 3 ? rs[3] : rs[4];
+            for (uint32_t q = 0; q < nmax; q += U) {
+                uint32_t p[U];
+                bool ok[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    ok[u] = q + (uint32_t)u < n;
+                    p[u] = 0u;
+                    if (ok[u]) {
+                        while (left == 0u) {
+                            ++k;
+                            left = k == 1 ? rl[1] : k == 2 ? rl[2] : k == 3 ? rl[3] : rl[4];
+                            pos = k == 1 ? rs[1] : k == 2 ? rs[2] : k == 3 ? rs[3] : rs[4];
+                        }
+                        p[u] = pos;
+                        ++pos;
+                        --left;
                     }
-                    hits += test(pa4, ma.x, ma.y, ma.z, ma.w, pos);
-                    ++pos;
-                    --left;
+                }
+                uint32_t o[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) o[u] = s.hkey[p[u]] & 0x3FFFu;
+                uint4 mb[U];
+                float4 pb[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    mb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
+                    pb[u] = hash_geom_pos<STAGED>(md, s, o[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const bool pass = mb[u].x != ma.x && !((ma.w & mb[u].z) == 0 && (mb[u].w & ma.z) == 0);
+                    const f3 diff = sub(xyz(pb[u]), xyz(pa4));
+                    const float min_dist = pa4.w + pb[u].w + 0.1f;
+                    const bool near = !(dot(diff, diff) >= min_dist * min_dist);
+                    const bool plane = ma.y == GEOM_PLANE || mb[u].y == GEOM_PLANE;
+                    hits += (ok[u] && pass && (plane || near)) ? 1u : 0u;
                 }
             }
             continue;
         }
-        // Two candidates per lane and trip (t and t + 64), their searches side by side.
-        auto deal = [&](uint32_t t, uint32_t olo) {
-            const int ow = (int)olo;
-            uint32_t u = t - ((uint32_t)__shfl((int)inc, ow) - (uint32_t)__shfl((int)n, ow));
-            uint32_t pos = 0;
-            bool found = false;
+        // Four candidates per lane and trip (t, t + 64, t + 128, t + 192), each stage of the
+        // four side by side: the owners (the first lane whose inclusive prefix exceeds t), the
+        // candidates' places in their owners' runs, the owners' geoms, the reads, the tests.
+        constexpr int D = 4;
+        for (uint32_t t0 = 0; t0 < T; t0 += (uint32_t)D * kWave) {
+            uint32_t tt[D], lo[D], hi[D];
 #pragma unroll
-            for (int k = 0; k < R; ++k) {
-                const uint32_t len = (uint32_t)__shfl((int)rl[k], ow);
-                const uint32_t st = (uint32_t)__shfl((int)rs[k], ow);
-                if (!found && u < len) { pos = st + u; found = true; }
-                if (!found) u -= len;
-            }
-            float4 pa;
-            uint4 mo;
-            if (STAGED) {  // the owner's geom from the staged arrays
-                const uint32_t go = (uint32_t)__shfl((int)ga, ow);
-                pa = hash_geom_pos<STAGED>(md, s, go);
-                mo = hash_geom_meta<STAGED>(md, hmeta, go);
-            } else {
-                pa = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
-                mo = make_uint4((uint32_t)__shfl((int)ma.x, ow), (uint32_t)__shfl((int)ma.y, ow),
-                                (uint32_t)__shfl((int)ma.z, ow), (uint32_t)__shfl((int)ma.w, ow));
-            }
-            return (t < T && found) ? test(pa, mo.x, mo.y, mo.z, mo.w, pos) : 0u;
-        };
-        for (uint32_t t0 = 0; t0 < T; t0 += 2u * kWave) {
-            const uint32_t tA = t0 + (uint32_t)lane, tB = tA + kWave;
-            // Owners: the first lane whose inclusive prefix exceeds t.
-            uint32_t loA = 0, hiA = kWave - 1, loB = 0, hiB = kWave - 1;
+            for (int u = 0; u < D; ++u) { tt[u] = t0 + (uint32_t)u * kWave + (uint32_t)lane; lo[u] = 0u; hi[u] = kWave - 1; }
             for (int step = 0; step < 6; ++step) {
-                const uint32_t midA = (loA + hiA) >> 1, midB = (loB + hiB) >> 1;
-                const uint32_t vA = (uint32_t)__shfl((int)inc, (int)midA), vB = (uint32_t)__shfl((int)inc, (int)midB);
-                if (vA > tA) hiA = midA; else loA = midA + 1u;
-                if (vB > tB) hiB = midB; else loB = midB + 1u;
+#pragma unroll
+                for (int u = 0; u < D; ++u) {
+                    const uint32_t mid = (lo[u] + hi[u]) >> 1;
+                    const uint32_t v = (uint32_t)__shfl((int)inc, (int)mid);
+                    if (v > tt[u]) hi[u] = mid; else lo[u] = mid + 1u;
+                }
             }
-            hits += deal(tA, loA) + deal(tB, loB);
+            uint32_t p[D];
+            bool ok[D];
+            float4 pa[D];
+            uint4 mo[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int ow = (int)lo[u];
+                uint32_t c = tt[u] - ((uint32_t)__shfl((int)inc, ow) - (uint32_t)__shfl((int)n, ow));
+                uint32_t pos = 0;
+                bool found = false;
+#pragma unroll
+                for (int k = 0; k < R; ++k) {
+                    const uint32_t len = (uint32_t)__shfl((int)rl[k], ow);
+                    const uint32_t st = (uint32_t)__shfl((int)rs[k], ow);
+                    if (!found && c < len) { pos = st + c; found = true; }
+                    if (!found) c -= len;
+                }
+                p[u] = pos;
+                ok[u] = tt[u] < T && found;
+                if (STAGED) {  // the owner's geom from the staged arrays
+                    const uint32_t go = (uint32_t)__shfl((int)ga, ow);
+                    pa[u] = hash_geom_pos<STAGED>(md, s, go);
+                    mo[u] = hash_geom_meta<STAGED>(md, hmeta, go);
+                } else {
+                    pa[u] = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
+                    mo[u] = make_uint4((uint32_t)__shfl((int)ma.x, ow), (uint32_t)__shfl((int)ma.y, ow),
+                                       (uint32_t)__shfl((int)ma.z, ow), (uint32_t)__shfl((int)ma.w, ow));
+                }
+            }
+            uint32_t o[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u) o[u] = s.hkey[p[u]] & 0x3FFFu;
+            uint4 mb[D];
+            float4 pb[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                mb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
+                pb[u] = hash_geom_pos<STAGED>(md, s, o[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const bool pass = mb[u].x != mo[u].x && !((mo[u].w & mb[u].z) == 0 && (mb[u].w & mo[u].z) == 0);
+                const f3 diff = sub(xyz(pb[u]), xyz(pa[u]));
+                const float min_dist = pa[u].w + pb[u].w + 0.1f;
+                const bool near = !(dot(diff, diff) >= min_dist * min_dist);
+                const bool plane = mo[u].y == GEOM_PLANE || mb[u].y == GEOM_PLANE;
+                hits += (ok[u] && pass && (plane || near)) ? 1u : 0u;
+            }
         }
     }
     for (int d = 1; d < kWave; d <<= 1) hits += (uint32_t)__shfl_xor((int)hits, d);
