@@ -1275,7 +1275,10 @@ void step_kernel(StepArgs a) {
                 if (take_vb) s.vb[0] = s.vel[0];
             }
             for (uint32_t b = bf + sl; b < B; b += G) {
-                const float4 imi = md.invmi[b];
+                // The body's model records are read before any branch, so the reads are in
+                // flight together (the model may be in HBM).
+                const float4 imi = md.invmi[b], com = md.com[b];
+                const uint32_t fl = md.flags[b];
                 float4 P = s.pos[b], Q = s.quat[b];
                 if (take_vb) s.vb[b] = s.vel[b];
                 if (imi.x < 1e-8f) {
@@ -1285,10 +1288,10 @@ void step_kernel(StepArgs a) {
                     float mass = 1.0f / imi.x;
                     f3 force = mk3(a.gx * mass, a.gy * mass, a.gz * mass);
                     s.frc[b] = tof4(force, 0.0f);
-                    f3 cw = qrot(xyz(md.com[b]), toq(Q));
+                    f3 cw = qrot(xyz(com), toq(Q));
                     s.trq[b] = tof4(cross(cw, force), 0.0f);
                 }
-                if (md.flags[b] & 1u) {
+                if (fl & 1u) {
                     P = tof4(add(xyz(P), scale(xyz(s.vel[b]), a.dt)), 0.0f);
                     const q4 q = toq(Q);
                     f3 h = scale(scale(xyz(s.angvel[b]), a.dt), 0.5f);
@@ -1448,12 +1451,12 @@ void step_kernel(StepArgs a) {
         if (live && do_solve && !fuse) {
             for (uint32_t b = bf + sl; b < B; b += G) {
                 const float4 imi = md.invmi[b];
+                const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
                 if (imi.x < 1e-8f) {
                     if (SPLIT) { s.frc[b] = s.pos[b]; s.trq[b] = s.quat[b]; }  // the helper's pose copy
                     continue;
                 }
                 float4 f = s.frc[b], t = s.trq[b];
-                const uint32_t e0 = md.bjoff[b], e1 = md.bjoff[b + 1];
                 // The body's list entries and contributions are read four at a time (one LDS
                 // round trip each), then summed in list order.
                 for (uint32_t e = e0; e < e1; e += 4) {
@@ -2214,10 +2217,16 @@ void step_kernel(StepArgs a) {
             uint32_t kb = 0;
             for (uint32_t b = bf + sl; b < B; b += G, ++kb) {
                 if (HBM && ((early_bits >> kb) & 1u) != 0u) continue;
-                if (md.invmi[b].x < 1e-8f) continue;
-                const float4 v = tof4(scale(sub(xyz(s.pos[b]), xyz(s.ppos[b])), inv_dt), 0.0f);
+                const float imass = md.invmi[b].x;
+                // Poses in LDS are read beside the model record (both in flight together); in
+                // HBM only for the bodies that move.
+                float4 P, PP, Q, PQ;
+                if constexpr (!HBM) { P = s.pos[b]; PP = s.ppos[b]; Q = s.quat[b]; PQ = s.pquat[b]; }
+                if (imass < 1e-8f) continue;
+                if constexpr (HBM) { P = s.pos[b]; PP = s.ppos[b]; Q = s.quat[b]; PQ = s.pquat[b]; }
+                const float4 v = tof4(scale(sub(xyz(P), xyz(PP)), inv_dt), 0.0f);
                 s.vel[b] = v;
-                q4 dq = qmul(toq(s.quat[b]), qconj(toq(s.pquat[b])));
+                q4 dq = qmul(toq(Q), qconj(toq(PQ)));
                 if (dq.w < 0) dq = qneg(dq);
                 s.angvel[b] = tof4(scale(sscale(2.0f, xyz(dq)), inv_dt), 0.0f);
                 if (acc_here) {
