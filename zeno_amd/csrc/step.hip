@@ -550,10 +550,18 @@ __device__ __forceinline__ void solve_contact2(const Mdl& md, const Lds& s, uint
 // ---------------------------------------------------------------------------------------
 // narrow_phase, all_shaders.metal:751-894, one slot.
 // ---------------------------------------------------------------------------------------
+// AHEAD (model records in HBM): both geom records are read whole at the start, so their reads
+// are in flight together instead of some waiting behind the type tests.
+template <bool AHEAD>
 __device__ __forceinline__ void narrow_slot(const StepArgs& a, const Mdl& md, const Lds& s, ContactRec* c) {
     const uint32_t body_a = c->indices[0], body_b = c->indices[1];
-    const GeomRec& ga = md.geoms[c->indices[2]];
-    const GeomRec& gb = md.geoms[c->indices[3]];
+    GeomRec la, lb;
+    if constexpr (AHEAD) {
+        la = md.geoms[c->indices[2]];
+        lb = md.geoms[c->indices[3]];
+    }
+    const GeomRec& ga = AHEAD ? la : md.geoms[c->indices[2]];
+    const GeomRec& gb = AHEAD ? lb : md.geoms[c->indices[3]];
     const f3 pos_a = add(xyz(s.pos[body_a]), mk3(ga.pos_size0[0], ga.pos_size0[1], ga.pos_size0[2]));
     const f3 pos_b = add(xyz(s.pos[body_b]), mk3(gb.pos_size0[0], gb.pos_size0[1], gb.pos_size0[2]));
     const uint32_t type_a = ga.type_body[0], type_b = gb.type_body[0];
@@ -1845,10 +1853,10 @@ void step_kernel(StepArgs a) {
             }
             wave_sync<HBM>();
             if (live) {
-                for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.order[k]]);
+                for (uint32_t k = sl; k < n_live; k += G) narrow_slot<PL != PL_LDS>(a, md, s, &s.con[s.order[k]]);
             }
         } else if (live) {
-            for (uint32_t k = sl; k < n_live; k += G) narrow_slot(a, md, s, &s.con[s.perm[k]]);
+            for (uint32_t k = sl; k < n_live; k += G) narrow_slot<PL != PL_LDS>(a, md, s, &s.con[s.perm[k]]);
         }
         wave_sync<HBM>();
         // ---- G: match_cached_contacts (:1483-1544) ------------------------------------
