@@ -1,6 +1,7 @@
 """The benchmark configurations at their full sizes (Pendulum and Cartpole 1024 envs, Ant 4096,
 Humanoid 16384, the 64-body pile 8192), HIP step against the multithreaded CPU oracle on the
-same inputs, plus the size-independent invariants of the step over longer runs:
+same inputs, also at their benchmark lengths (1000 steps, the pile's 500), plus the
+size-independent invariants of the step over longer runs:
 unit quaternions, finite state, an untouched world body, the world-body observation
 constants, and never-decreasing contact counts (the step appends and never clears them)."""
 import numpy as np
@@ -45,4 +46,19 @@ def test_full_size_invariants(name, envs, steps):
             c = g.get_contact_counts()
             assert np.all(c >= counts_prev)
             counts_prev = c.copy()
+    g.close()
+
+
+@pytest.mark.parametrize("name,envs,steps", [("ant", 4096, 1000), ("humanoid", 16384, 1000), ("pile", 8192, 500)])
+def test_benchmark_length_parity(name, envs, steps):
+    """The configurations at their benchmark lengths (Ant 4096 x 1000 steps, Humanoid 16384 x
+    1000, the pile 8192 x 500), bit for bit against the oracle at four points along the run.
+    The first 100 steps' action rows are used over and over (the same rows on both sides)."""
+    g, o, acts = make_pair(name, envs, 100, seed=303)
+    for k in range(steps):
+        g.step(acts[k % 100])
+        o.step(acts[k % 100])
+        if (k + 1) % (steps // 4) == 0:
+            compare(gpu_arrays(g), oracle_arrays(o), **TOL)
+    assert np.all(np.isfinite(g.get_body_positions(zero_copy=False)))
     g.close()
