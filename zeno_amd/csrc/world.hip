@@ -28,10 +28,10 @@ namespace {
 __global__ void reset_envs_kernel(uint32_t E, uint32_t B, uint32_t J, uint32_t Jp, const uint8_t* mask,
                                   const float4* ipos, const float4* iquat, const float4* ivel, const float4* iang,
                                   float4* pos, float4* quat, float4* vel, float4* ang, float* jpos, float* jvel) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;  // E (B + J) may pass 2^32
     const uint32_t per = B + J;
-    if (i >= E * per) return;
-    const uint32_t e = i / per, k = i % per;
+    if (i >= (uint64_t)E * per) return;
+    const uint32_t e = (uint32_t)(i / per), k = (uint32_t)(i % per);
     if (mask && !mask[e]) return;
     if (k < B) {
         const size_t o = (size_t)e * B + k;
@@ -48,8 +48,8 @@ __global__ void reset_envs_kernel(uint32_t E, uint32_t B, uint32_t J, uint32_t J
 
 // Copies src into dst for the envs selected by mask (all envs when mask is null).
 __global__ void masked_copy_kernel(uint32_t E, uint32_t B, const uint8_t* mask, const float4* src, float4* dst) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= E * B) return;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)E * B) return;
     if (mask && !mask[i / B]) return;
     dst[i] = src[i];
 }
