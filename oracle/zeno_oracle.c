@@ -58,6 +58,12 @@
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
+/* The thread count of a call that passes none: OpenMP's default (OMP_NUM_THREADS, else the
+ * processor count) read once when the library loads. A call's count goes to its own loop
+ * only (num_threads clause), never to the process-wide setting, which would stay for every
+ * later call. */
+static int zo_default_threads = 1;
+__attribute__((constructor)) static void zo_read_default_threads(void) { zo_default_threads = omp_get_max_threads(); }
 #endif
 
 /* ------------------------------------------------------------------------------------
@@ -1063,8 +1069,7 @@ int zo_step(const ZoModel* m, ZoState* s, const float* actions, uint32_t substep
     const size_t B = m->num_bodies;
     const uint32_t A = m->num_actuators;
 #ifdef _OPENMP
-    if (nthreads > 0) omp_set_num_threads(nthreads);
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : zo_default_threads)
 #endif
     for (int64_t ei = (int64_t)env_begin; ei < (int64_t)env_end; ++ei) {
         uint32_t env = (uint32_t)ei;
@@ -1560,8 +1565,7 @@ int zo_detect_collision(const ZoCollider* a, const ZoCollider* b, ZoContactResul
 /* detectCollision over n pairs (the CPU baseline of the batched kernel); OpenMP over pairs. */
 void zo_detect_collisions(const ZoCollider* a, const ZoCollider* b, uint32_t n, ZoContactResult* out, int nthreads) {
 #ifdef _OPENMP
-    if (nthreads > 0) omp_set_num_threads(nthreads);
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : zo_default_threads)
 #endif
     for (int64_t i = 0; i < (int64_t)n; ++i) zo_detect_collision(&a[i], &b[i], &out[i]);
     (void)nthreads;
