@@ -384,3 +384,21 @@ def test_worlds_side_by_side_stay_independent():
     for g, _, _ in worlds:
         if g is not None:
             g.close()
+
+
+@pytest.mark.parametrize("xml", [
+    '<mujoco><worldbody><geom type="plane" size="5 5 0.1"/></worldbody></mujoco>',
+    '<mujoco><worldbody><body name="b" pos="0 0 1"><joint type="free"/><geom type="sphere" size="0.1"/></body>'
+    '</worldbody></mujoco>',
+    '<mujoco><worldbody><geom type="plane" size="5 5 0.1"/><body name="b" pos="0 0 0.05"><joint type="free"/>'
+    '<geom type="sphere" size="0.1"/></body></worldbody></mujoco>'], ids=["world_only", "free_body", "resting_body"])
+def test_smallest_scenes_match_oracle(xml):
+    """Scenes at the small end: the world body alone (a plane, nothing to move, no pair), one
+    free body with no geom to meet, and one free body resting in the plane; 5 envs, each step
+    against the oracle."""
+    g, o = pair_from_string(xml, 5)
+    for _ in range(6):
+        g.step(np.zeros((5, 0), np.float32))
+        o.step(None)
+        compare(gpu_arrays(g), oracle_arrays(o), **TOL)
+    g.close()
