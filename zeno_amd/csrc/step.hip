@@ -816,9 +816,10 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
 // the row y + 1 at z, and the rows y - 1, y, y + 1 at z + 1 (x - 1 .. x + 1 each). The pair
 // tests are those of hash_pairs_of; each is symmetric in its two geoms (the difference's
 // sign does not change its square, nor the radii's order their sum), so the earlier geom
-// may take either role. The runs' nine ends are found by interleaved binary searches, then
-// the wave's candidates are dealt out 64 at a time, each lane finding its candidate's run
-// by a search over the lanes' prefix sums, so a crowded cell does not hold the wave up.
+// may take either role. The runs' nine ends are found by interleaved binary searches; then
+// each lane walks its own candidates, or, when one lane holds more than twice the mean, the
+// wave's candidates are dealt out four per lane at a time, each lane finding its candidate's
+// run by a search over the lanes' prefix sums, so a crowded cell does not hold the wave up.
 template <bool STAGED>
 __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, int lane) {
     constexpr int R = 5;
