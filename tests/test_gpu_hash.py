@@ -62,7 +62,6 @@ def test_hash_key_sort_sizes(num_bodies):
     (padded to 2048: the network runs in LDS instead of registers) and 1501. Piles of that
     many bodies at the 601-body pile's density, every step against the oracle, cell ids
     included."""
-    import os
     from oracle.oracle import OracleWorld
     from zeno_amd.model import load_model
     from zeno_amd.scenes import pile_initial_state, pile_mjcf
