@@ -28,9 +28,9 @@ struct EnvLds {
     // (u32[M] each, at byte 8M and 12M) share ppen.
     uint32_t vlist, lst, loff;
     // Spatial-hash broad phase (scenes above kHashMinGeoms geoms), on skey as well: hkey
-    // u32[Gp] (cell << 14 | geom, sorted), hcell u32[G] (cell of each geom), hpos/hmeta
-    // (world centre and radius, body / type / masks of each geom).
-    uint32_t hkey, hcell, hpos;
+    // u32[hash_keys(G)] (cell << 14 | geom, sorted), then, staged, hpos float4[G] (world
+    // centre and radius) and hmeta u32[G] (the model's compact geom word) of each geom.
+    uint32_t hkey, hpos;
     uint32_t bmask;  // contact levels: u64[B][ceil(M/64)] slot masks per body
     // Joint solve records with compliance / dt^2 filled in: a per-environment copy used
     // when the model blob is read in place from HBM.
@@ -51,16 +51,19 @@ inline uint32_t hash_pad(uint32_t G) { uint32_t p = 1; while (p < G) p <<= 1; re
 // the slots' keys (on skey) and logical positions (on order), both padded to a power of two.
 constexpr uint32_t kRankSortMax = 8;
 inline uint32_t sort_pad(uint32_t M) { return hash_pad(M); }
-// Spatial-hash scratch (on the sort-key region): hkey u32[Gp], hcell u32[G], then 16-B
-// aligned hpos float4[G] (world centre, radius) and hmeta uint4[G] (body, type, contype
-// mask, conaffinity group) of every geom, staged once per substep for the queries.
-inline uint32_t hash_hcell_off(uint32_t G) { return 4 * hash_pad(G); }
-inline uint32_t hash_hpos_off(uint32_t G) { return align16(4 * hash_pad(G) + 4 * G); }
+// Spatial-hash scratch (on the sort-key region): the sort keys, then 16-B aligned hpos
+// float4[G] (world centre, radius) and hmeta u32[G] (the model's compact geom word: body,
+// plane flag, filter class) of every geom, staged once per substep for the queries. Up to
+// 1024 keys are sorted in registers and only the G real keys are stored; longer lists are
+// sorted in LDS, padded to a power of two.
+constexpr uint32_t kHashClasses = 32;  // filter classes the model's rows describe
+inline uint32_t hash_keys(uint32_t G) { return hash_pad(G) <= 1024u ? G : hash_pad(G); }
+inline uint32_t hash_hpos_off(uint32_t G) { return align16(4 * hash_keys(G)); }
 // staged: with hpos / hmeta (the layout for working sets in HBM, where reading the model
 // records and body poses in the queries would go to global memory).
 inline uint32_t hash_bytes_for(uint32_t G, bool staged) {
     if (G <= kHashMinGeoms) return 0;
-    return staged ? hash_hpos_off(G) + 32 * G : 4 * (hash_pad(G) + G);
+    return staged ? hash_hpos_off(G) + 20 * G : 4 * hash_keys(G);
 }
 
 // G = geom count (hash arrays only when G > kHashMinGeoms); jrec_bytes = size of the joint
@@ -85,9 +88,9 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
     L.order = take(2 * sort_pad(M));
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;  // 16 * M >= 2 * (M + 2) for M >= 1
-    L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
+    L.hkey = L.skey;
     // The queries stage nothing when the working set is in LDS; in HBM (placement 3) they
-    // stage each geom's centre and metadata after the sorted keys and cells.
+    // stage each geom's centre and compact word after the sorted keys.
     L.hpos = L.skey + (hash_staged && G > kHashMinGeoms ? hash_hpos_off(G) : 0);
     // Per-body bit masks of the valid contact slots touching the body (u64[B][ceil(M/64)]),
     // on the force and torque arrays (dead from integration to the next substep) when they fit.
@@ -108,25 +111,35 @@ inline EnvLds make_env_lds(uint32_t B, uint32_t Jp, uint32_t N, uint32_t M, uint
 // their own; only their offsets in the returned EnvLds are meaningful. With masks_in_lds
 // false the body slot masks stay in the HBM working set (bmask = kInHbm): scenes with many
 // bodies and long contact lists, whose masks alone would not fit.
+// With the spatial hash the previous-contact snapshot shares the sort-key region too, above
+// the sort keys, level lists and body masks: the kernel takes it after the broad phase (the
+// hash's arrays are dead by then), so the region serves both and the layout stays small
+// enough for two environments per SIMD.
 constexpr uint32_t kInHbm = 0xFFFFFFFFu;
 inline EnvLds make_env_lds_small(uint32_t B, uint32_t Jp, uint32_t M, uint32_t G = 0, bool stage_geoms = false,
                                  bool masks_in_lds = true) {
     EnvLds L{};
     uint32_t o = 0;
     auto take = [&](uint32_t bytes) { uint32_t r = o; o = align16(o + bytes); return r; };
+    const bool hash = G > kHashMinGeoms;
     const uint32_t hash_bytes = hash_bytes_for(G, true);
     L.con = take(64 * M);
     L.perm = take(2 * M);
     const uint32_t mask_bytes = masks_in_lds ? 8 * ((M + 63) / 64) * B : 0u;
     // bmask follows vlist and lst on the sort-key region: the levels run after the sort and
     // the broad phase are done with it.
-    L.skey = take(std::max(std::max(std::max(4 * M + mask_bytes, 4 * sort_pad(M)), 16 * Jp), hash_bytes));
-    L.ppen = take(16 * M); L.pimp = take(16 * M);
+    const uint32_t lists = align16(std::max(std::max(4 * M + mask_bytes, 4 * sort_pad(M)), 16 * Jp));
+    L.skey = take(std::max(hash ? lists + 32 * M : lists, hash_bytes));
+    if (hash) {
+        L.ppen = L.skey + lists; L.pimp = L.ppen + 16 * M;
+    } else {
+        L.ppen = take(16 * M); L.pimp = take(16 * M);
+    }
     L.order = take(2 * sort_pad(M));
     L.vlist = L.skey; L.lst = L.skey + 2 * M;
     L.loff = L.ppen;
-    L.hkey = L.skey; L.hcell = L.skey + (G > kHashMinGeoms ? hash_hcell_off(G) : 0);
-    L.hpos = L.skey + (G > kHashMinGeoms ? hash_hpos_off(G) : 0);
+    L.hkey = L.skey;
+    L.hpos = L.skey + (hash ? hash_hpos_off(G) : 0);
     L.bmask = masks_in_lds ? L.skey + 4 * M : kInHbm;
     if (stage_geoms) { L.gst = take(16 * G); L.gmeta = take(4 * G); }
     L.misc = take(16);
@@ -250,6 +263,44 @@ inline void build_joint_program(const std::vector<ConstraintRec>& tmpl, const st
 // Joints acting on each body for apply_joint_forces (all_shaders.metal:122-190), in
 // ascending joint order: entry = joint index | bit 30 (body is the joint's parent, the
 // contribution is negated) | bit 31 (prismatic: force, else torque). Body 0 gets none.
+// The spatial hash's compact geom words and filter rows (ModelLayout.hmeta / hrow): a dense
+// id per body that owns a geom (at most kHashMaxGeoms of them, so 14 bits), the plane flag,
+// and a class per distinct (contype, conaffinity) pair in order of first appearance. The
+// queries compare the ids for "different bodies" and test the filter of :493-522,
+// (contype_a & conaffinity_b) || (contype_b & conaffinity_a), as bit c of row k for classes
+// k and c. Returns false when there are more than kHashClasses classes: the rows are then
+// unused and the queries read the masks from the geom records.
+inline bool build_hash_words(const std::vector<GeomRec>& geoms, std::vector<uint32_t>& meta, std::vector<uint32_t>& rows) {
+    std::vector<uint32_t> body_id, ct, ca;
+    meta.assign(geoms.size(), 0u);
+    rows.assign(kHashClasses, 0u);
+    uint32_t ids = 0;
+    bool fits = true;
+    for (size_t g = 0; g < geoms.size(); ++g) {
+        const GeomRec& gr = geoms[g];
+        const uint32_t body = gr.type_body[1];
+        if (body >= body_id.size()) body_id.resize((size_t)body + 1, 0xFFFFFFFFu);
+        if (body_id[body] == 0xFFFFFFFFu) body_id[body] = ids++;
+        uint32_t cls = 0;
+        if (fits) {
+            while (cls < ct.size() && !(ct[cls] == gr.type_body[3] && ca[cls] == gr.type_body[2])) ++cls;
+            if (cls == ct.size()) {
+                if (cls == kHashClasses) fits = false;
+                else { ct.push_back(gr.type_body[3]); ca.push_back(gr.type_body[2]); }
+            }
+        }
+        meta[g] = (body_id[body] & 0x3FFFu) | (gr.type_body[0] == GEOM_PLANE ? 1u << 14 : 0u) | ((fits ? cls : 0u) << 15);
+    }
+    if (!fits) {
+        for (uint32_t& w : meta) w &= 0x7FFFu;
+        return false;
+    }
+    for (size_t k = 0; k < ct.size(); ++k)
+        for (size_t c = 0; c < ct.size(); ++c)
+            if ((ct[k] & ca[c]) != 0u || (ct[c] & ca[k]) != 0u) rows[k] |= 1u << c;
+    return true;
+}
+
 inline void build_body_joint_lists(const std::vector<JointRec>& joints, uint32_t B, std::vector<uint32_t>& off,
                                    std::vector<uint32_t>& ent) {
     off.assign(B + 1, 0);
@@ -280,6 +331,11 @@ struct ModelLayout {
     uint32_t jrec;               // float4[kJRecQuads * R] joint solve records
     uint32_t jphase;             // JointPhase[nph]
     uint32_t bjoff, bjl;         // u32[B + 1] offsets into u32[2J]: joints acting on each body
+    // Spatial hash (G > kHashMinGeoms) only: hmeta u32[G], each geom's compact word for the
+    // queries (bits 0-13 a dense id of its body, bit 14 plane, bits 15-19 its filter class),
+    // and hrow u32[32], the classes' filter rows (bit c of row k: a geom of class k and one
+    // of class c pass the contype / conaffinity test), valid when StepArgs.hrows is set.
+    uint32_t hmeta, hrow;
     uint32_t bytes;              // total, multiple of 16
 };
 
@@ -293,6 +349,8 @@ inline ModelLayout make_model_layout(uint32_t B, uint32_t J, uint32_t G, uint32_
     L.acts = take(32 * A); L.sensors = take(32 * S);
     L.jrec = take(16 * kJRecQuads * nrec); L.jphase = take(16 * nph);
     L.bjoff = take(4 * (B + 1)); L.bjl = take(4 * 2 * J);
+    const bool hash = G > kHashMinGeoms;
+    L.hmeta = take(hash ? 4 * G : 0); L.hrow = take(hash ? 4 * kHashClasses : 0);
     L.bytes = o;
     return L;
 }
@@ -301,6 +359,9 @@ struct StepArgs {
     // Sizes. G = geoms; Gp = G rounded up to a power of two (hash mode).
     uint32_t E, B, J, Jp, A, S, obsp, N, nrec, njph, M, P, G, Gp;
     uint32_t hash;  // 1: spatial-hash broad phase (G > kHashMinGeoms), 0: candidate pair list
+    // 1: at most kHashClasses distinct (contype, conaffinity) pairs, so the hash queries test
+    // the filter by the model's class rows; 0: they read both geoms' masks from the records.
+    uint32_t hrows;
     uint32_t ext_contacts;  // 1: pairs the reference's narrow phase leaves invalid use detectCollision
     // 1: sort the contact list in the first substep even if no append took a slot below M (the
     // host changed the counts, exposing slots whose order the last sort did not cover).

@@ -46,8 +46,8 @@ struct Lds {
     float4 *ppen, *pimp;  // prev snapshot: position_pen; impulses.xyz with the pair key in .w
     float4* jw;  // per-joint force/torque contributions (stage C), aliased on skey
     uint16_t *order, *vlist, *lst, *loff;
-    uint32_t *hkey, *hcell;  // spatial hash, aliased on skey
-    float4* hpos;            // spatial hash: geom world centre + radius (then uint4 meta[G])
+    uint32_t* hkey;          // spatial hash, aliased on skey
+    float4* hpos;            // spatial hash: geom world centre + radius (then u32 meta[G])
     uint32_t *vbod, *prv;    // contact levels: per-slot dynamic bodies and predecessors (on ppen)
     unsigned long long* bmask;  // contact levels: per-body slot masks
     float4* jrec;            // per-environment solve records (model records in HBM)
@@ -80,7 +80,6 @@ __device__ __forceinline__ Lds bind_lds(unsigned char* base, const EnvLds& L) {
     s.vbod = (uint32_t*)(base + L.ppen + 0u);  // placed by bind_levels
     s.prv = s.vbod;
     s.bmask = (unsigned long long*)(base + L.bmask);
-    s.hcell = (uint32_t*)(base + L.hcell);
     s.jrec = (float4*)(base + L.jrec);
     s.gst = (float4*)(base + L.gst);
     s.gmeta = (uint32_t*)(base + L.gmeta);
@@ -101,7 +100,6 @@ __device__ __forceinline__ void bind_small(Lds& s, unsigned char* base, const En
     s.lst = (uint16_t*)(base + L.lst);
     s.loff = (uint16_t*)(base + L.loff);
     s.hkey = (uint32_t*)(base + L.hkey);
-    s.hcell = (uint32_t*)(base + L.hcell);
     s.hpos = (float4*)(base + L.hpos);
     if (L.bmask != kInHbm) s.bmask = (unsigned long long*)(base + L.bmask);  // else: in the HBM working set
     s.gst = (float4*)(base + L.gst);
@@ -129,6 +127,7 @@ struct Mdl {
     const float4* jrec;
     const JointPhase* jph;
     const uint32_t *bjoff, *bjl;
+    const uint32_t *hmeta, *hrow;
 };
 
 __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const ModelLayout& L) {
@@ -145,6 +144,8 @@ __device__ __forceinline__ Mdl bind_model(const unsigned char* base, const Model
     m.jph = (const JointPhase*)(base + L.jphase);
     m.bjoff = (const uint32_t*)(base + L.bjoff);
     m.bjl = (const uint32_t*)(base + L.bjl);
+    m.hmeta = (const uint32_t*)(base + L.hmeta);
+    m.hrow = (const uint32_t*)(base + L.hrow);
     return m;
 }
 
@@ -725,21 +726,39 @@ __device__ __forceinline__ float4 hash_geom_pos(const Mdl& md, const Lds& s, uin
     return tof4(add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2])), gr.pos_size0[3]);
 }
 template <bool STAGED>
-__device__ __forceinline__ uint4 hash_geom_meta(const Mdl& md, const uint4* hmeta, uint32_t g) {
+__device__ __forceinline__ uint32_t hash_geom_meta(const Mdl& md, const uint32_t* hmeta, uint32_t g) {
     if (STAGED) return hmeta[g];
+    return md.hmeta[g];
+}
+// Fields of a geom's compact word (ModelLayout.hmeta).
+__device__ __forceinline__ uint32_t hw_body(uint32_t w) { return w & 0x3FFFu; }
+__device__ __forceinline__ bool hw_plane(uint32_t w) { return ((w >> 14) & 1u) != 0u; }
+__device__ __forceinline__ uint32_t hw_class(uint32_t w) { return (w >> 15) & 31u; }
+// A geom's side of the contype / conaffinity test (:493-522): its class row, or, when the
+// classes do not fit the rows, (contype, conaffinity) from its record.
+__device__ __forceinline__ uint2 hash_filter_of(const StepArgs& a, const Mdl& md, uint32_t g, uint32_t w) {
+    if (a.hrows) return make_uint2(md.hrow[hw_class(w)], 0u);
     const GeomRec& gr = md.geoms[g];
-    return make_uint4(gr.type_body[1], gr.type_body[0], gr.type_body[2], gr.type_body[3]);
+    return make_uint2(gr.type_body[3], gr.type_body[2]);
+}
+// (contype_a & conaffinity_b) || (contype_b & conaffinity_a) for the geom of filter words fa
+// and geom o of word w.
+__device__ __forceinline__ bool hash_filter_pass(const StepArgs& a, const Mdl& md, uint2 fa, uint32_t o, uint32_t w) {
+    if (a.hrows) return ((fa.x >> hw_class(w)) & 1u) != 0u;
+    const GeomRec& gr = md.geoms[o];
+    return ((fa.x & gr.type_body[2]) | (gr.type_body[3] & fa.y)) != 0u;
 }
 
 template <bool STAGED>
-__device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, uint32_t g, bool emit,
+__device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& md, const Lds& s, const uint32_t* hmeta, uint32_t g, bool emit,
                                   uint32_t slot) {
     const float4 pa4 = hash_geom_pos<STAGED>(md, s, g);
-    const uint4 ma = hash_geom_meta<STAGED>(md, hmeta, g);
-    const uint32_t body_a = ma.x, type_a = ma.y, mask_a = ma.z, group_a = ma.w;
+    const uint32_t wa = hash_geom_meta<STAGED>(md, hmeta, g);
+    const uint2 fa = hash_filter_of(a, md, g, wa);
     const f3 pa = xyz(pa4);
     const float ra = pa4.w;
-    const uint32_t id = s.hcell[g];
+    // The geom's cell, from the same centre the staging hashed.
+    const uint32_t id = hash_axis(pa.x) + hash_axis(pa.y) * 64u + hash_axis(pa.z) * 4096u;
     const int cx = (int)(id & 63u), cy = (int)((id >> 6) & 63u), cz = (int)(id >> 12);
     const uint32_t xlo = cx > 0 ? (uint32_t)cx - 1u : 0u, xhi = cx < 63 ? (uint32_t)cx + 1u : 63u;
     // The nine rows' first positions (first key whose cell is >= the row's first cell), by
@@ -787,11 +806,10 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
                 if (key > last) break;
                 const uint32_t o = key & 0x3FFFu;
                 if (o <= g) continue;
-                const uint4 mb = hash_geom_meta<STAGED>(md, hmeta, o);
-                const uint32_t body_b = mb.x;
-                if (body_a == body_b) continue;
-                if ((group_a & mb.z) == 0 && (mb.w & mask_a) == 0) continue;
-                if (!(type_a == GEOM_PLANE || mb.y == GEOM_PLANE)) {
+                const uint32_t wb = hash_geom_meta<STAGED>(md, hmeta, o);
+                if (hw_body(wa) == hw_body(wb)) continue;
+                if (!hash_filter_pass(a, md, fa, o, wb)) continue;
+                if (!(hw_plane(wa) || hw_plane(wb))) {
                     const float4 pb4 = hash_geom_pos<STAGED>(md, s, o);
                     const f3 diff = sub(xyz(pb4), pa);
                     const float min_dist = ra + pb4.w + 0.1f;
@@ -799,7 +817,7 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
                 }
                 if (emit && slot + hits < a.M) {
                     uint32_t* idx = s.con[s.perm[slot + hits]].indices;
-                    idx[0] = body_a; idx[1] = body_b; idx[2] = g; idx[3] = o;
+                    idx[0] = md.geoms[g].type_body[1]; idx[1] = md.geoms[o].type_body[1]; idx[2] = g; idx[3] = o;
                 }
                 ++hits;
             }
@@ -821,7 +839,7 @@ __device__ __forceinline__ uint32_t hash_pairs_of(const StepArgs& a, const Mdl& 
 // wave's candidates are dealt out four per lane at a time, each lane finding its candidate's
 // run by a search over the lanes' prefix sums, so a crowded cell does not hold the wave up.
 template <bool STAGED>
-__device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const Mdl& md, const Lds& s, const uint4* hmeta, int lane) {
+__device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const Mdl& md, const Lds& s, const uint32_t* hmeta, int lane) {
     constexpr int R = 5;
     const uint32_t NG = a.G;
     uint32_t hits = 0;
@@ -884,7 +902,8 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
         }
         const uint32_t T = (uint32_t)__shfl((int)inc, kWave - 1);
         const float4 pa4 = mine ? hash_geom_pos<STAGED>(md, s, ga) : make_float4(0, 0, 0, 0);
-        const uint4 ma = mine ? hash_geom_meta<STAGED>(md, hmeta, ga) : make_uint4(0, 0, 0, 0);
+        const uint32_t wa = mine ? hash_geom_meta<STAGED>(md, hmeta, ga) : 0u;
+        const uint2 fa = mine ? hash_filter_of(a, md, ga, wa) : make_uint2(0u, 0u);
         // Balanced rounds (no lane with more than twice the mean's chunks) walk each lane's own
         // runs; others deal the candidates out.
         uint32_t nmax = n;
@@ -920,20 +939,23 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
                 uint32_t o[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) o[u] = s.hkey[p[u]] & 0x3FFFu;
-                uint4 mb[U];
+                uint32_t wb[U];
                 float4 pb[U];
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    mb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
+                    wb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
                     pb[u] = hash_geom_pos<STAGED>(md, s, o[u]);
                 }
+                bool fp[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) fp[u] = hash_filter_pass(a, md, fa, o[u], wb[u]);
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const bool pass = mb[u].x != ma.x && !((ma.w & mb[u].z) == 0 && (mb[u].w & ma.z) == 0);
+                    const bool pass = hw_body(wb[u]) != hw_body(wa) && fp[u];
                     const f3 diff = sub(xyz(pb[u]), xyz(pa4));
                     const float min_dist = pa4.w + pb[u].w + 0.1f;
                     const bool near = !(dot(diff, diff) >= min_dist * min_dist);
-                    const bool plane = ma.y == GEOM_PLANE || mb[u].y == GEOM_PLANE;
+                    const bool plane = hw_plane(wa) || hw_plane(wb[u]);
                     hits += (ok[u] && pass && (plane || near)) ? 1u : 0u;
                 }
             }
@@ -958,7 +980,8 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
             uint32_t p[D];
             bool ok[D];
             float4 pa[D];
-            uint4 mo[D];
+            uint32_t wo[D];
+            uint2 fo[D];
 #pragma unroll
             for (int u = 0; u < D; ++u) {
                 const int ow = (int)lo[u];
@@ -977,30 +1000,33 @@ __device__ __forceinline__ uint32_t hash_count_forward(const StepArgs& a, const 
                 if (STAGED) {  // the owner's geom from the staged arrays
                     const uint32_t go = (uint32_t)__shfl((int)ga, ow);
                     pa[u] = hash_geom_pos<STAGED>(md, s, go);
-                    mo[u] = hash_geom_meta<STAGED>(md, hmeta, go);
+                    wo[u] = hash_geom_meta<STAGED>(md, hmeta, go);
                 } else {
                     pa[u] = make_float4(__shfl(pa4.x, ow), __shfl(pa4.y, ow), __shfl(pa4.z, ow), __shfl(pa4.w, ow));
-                    mo[u] = make_uint4((uint32_t)__shfl((int)ma.x, ow), (uint32_t)__shfl((int)ma.y, ow),
-                                       (uint32_t)__shfl((int)ma.z, ow), (uint32_t)__shfl((int)ma.w, ow));
+                    wo[u] = (uint32_t)__shfl((int)wa, ow);
                 }
+                fo[u] = make_uint2((uint32_t)__shfl((int)fa.x, ow), (uint32_t)__shfl((int)fa.y, ow));
             }
             uint32_t o[D];
 #pragma unroll
             for (int u = 0; u < D; ++u) o[u] = s.hkey[p[u]] & 0x3FFFu;
-            uint4 mb[D];
+            uint32_t wb[D];
             float4 pb[D];
 #pragma unroll
             for (int u = 0; u < D; ++u) {
-                mb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
+                wb[u] = hash_geom_meta<STAGED>(md, hmeta, o[u]);
                 pb[u] = hash_geom_pos<STAGED>(md, s, o[u]);
             }
+            bool fp[D];
+#pragma unroll
+            for (int u = 0; u < D; ++u) fp[u] = hash_filter_pass(a, md, fo[u], o[u], wb[u]);
 #pragma unroll
             for (int u = 0; u < D; ++u) {
-                const bool pass = mb[u].x != mo[u].x && !((mo[u].w & mb[u].z) == 0 && (mb[u].w & mo[u].z) == 0);
+                const bool pass = hw_body(wb[u]) != hw_body(wo[u]) && fp[u];
                 const f3 diff = sub(xyz(pb[u]), xyz(pa[u]));
                 const float min_dist = pa[u].w + pb[u].w + 0.1f;
                 const bool near = !(dot(diff, diff) >= min_dist * min_dist);
-                const bool plane = mo[u].y == GEOM_PLANE || mb[u].y == GEOM_PLANE;
+                const bool plane = hw_plane(wo[u]) || hw_plane(wb[u]);
                 hits += (ok[u] && pass && (plane || near)) ? 1u : 0u;
             }
         }
@@ -1039,6 +1065,9 @@ __attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs a) {
     constexpr int G = kWave / EPW;
     constexpr bool HBM = PL >= PL_ALL_HBM;  // working set in HBM
+    // Placement 2 with the spatial hash keeps the previous-contact snapshot on the hash's
+    // arrays (make_env_lds_small): it is taken after the broad phase.
+    constexpr bool LATE_SNAP = HASH && PL == PL_ALL_HBM;
     static_assert(PL == PL_LDS || EPW == 1, "model records in HBM run one environment per workgroup");
     static_assert(!HASH || EPW == 1, "the spatial hash runs one environment per workgroup");
     static_assert(!GROUP || EPW == 1, "type-grouped narrow phase: one environment per workgroup");
@@ -1060,6 +1089,10 @@ void step_kernel(StepArgs a) {
     unsigned char* const env_base = HBM ? a.work + (size_t)wave_id * a.lds.bytes
                                         : smem + (PL == PL_LDS ? a.ml.bytes : 0u) + grp * EPW * a.lds.bytes;
     Lds s = bind_lds(env_base + le * a.lds.bytes, a.lds);
+    // The HBM working set's own snapshot arrays, unused by placement 2 but for a substep whose
+    // appends may wrap the count past 2^32 (LATE_SNAP below).
+    float4* const hppen = s.ppen;
+    float4* const hpimp = s.pimp;
     if (PL == PL_ALL_HBM) bind_small(s, smem, a.lds_small);  // PL_WORK_HBM: all of it in a.work
     bind_levels(s, a.M);
     Mdl md = bind_model(PL == PL_LDS ? smem : (const unsigned char*)a.model, a.ml);
@@ -1262,17 +1295,26 @@ void step_kernel(StepArgs a) {
         // ---- Previous-contact snapshot (cache_contacts of the last substep) -----------
         // A split group's helper takes it after the first barrier of the substep (with the
         // contact list's LDS copy in the first substep), so the solver never waits for it.
-        auto snapshot = [&]() {
+        // Taken after the broad phase (LATE_SNAP), its slots at or past the count the broad
+        // phase started from (`kept`) may hold appends: a list whose count the host lowered or
+        // reset before this call. The first substep reads those from the call's list in HBM,
+        // as loaded (the permutation is still the identity); in later substeps the snapshot's
+        // slots all lie below that count, where no append lands unless the count wraps past
+        // 2^32: a substep that may wrap takes the snapshot first, into the HBM working set,
+        // and copies it into place after the broad phase.
+        auto snapshot = [&](uint32_t kept, float4* dpen, float4* dimp) {
             const uint32_t pn = pcount < M ? pcount : M;
             const bool from_det = step == 0 && detached;
             for (uint32_t k = sl; k < pn; k += G) {
-                const ContactRec* r = from_det ? &a.prev_contacts[(size_t)env * M + k] : &s.con[s.perm[k]];
-                s.ppen[k] = *(const float4*)r->position_pen;
-                s.pimp[k] = make_float4(r->impulses[0], r->impulses[1], r->impulses[2],
-                                        __uint_as_float(pair_key(r->indices[0], r->indices[1])));
+                const bool from_list = LATE_SNAP && k >= kept;
+                const ContactRec* r = from_det ? &a.prev_contacts[(size_t)env * M + k] : from_list ? &gc[k] : &s.con[s.perm[k]];
+                dpen[k] = *(const float4*)r->position_pen;
+                dimp[k] = make_float4(r->impulses[0], r->impulses[1], r->impulses[2],
+                                      __uint_as_float(pair_key(r->indices[0], r->indices[1])));
             }
         };
-        if (!SPLIT && live) snapshot();
+        const bool snap_first = LATE_SNAP && (uint64_t)count + (uint64_t)a.G * (uint64_t)(a.G - 1u) / 2u > 0xFFFFFFFFull;
+        if (!SPLIT && (!LATE_SNAP || snap_first) && live) snapshot(M, snap_first ? hppen : s.ppen, snap_first ? hpimp : s.pimp);
         // Stage B (below), one text for the two places it runs from.
         const bool take_vb = alias && step == 0;  // aliased: the velocity at call start
         auto stage_b = [&]() {
@@ -1514,7 +1556,7 @@ void step_kernel(StepArgs a) {
                         s.perm[k] = (uint16_t)k;
                     }
                 }
-                snapshot();
+                snapshot(M, s.ppen, s.pimp);
             }
         }
         // ---- E: broad_phase (S1), :468-533, or the spatial hash, :556-703 -------------
@@ -1527,20 +1569,22 @@ void step_kernel(StepArgs a) {
         Lds& s = sp;
         const uint32_t count_before = count;
         if (HASH) {
-            uint4* const hmeta = (uint4*)(s.hpos + a.G);
-            // Cells (broad_phase_count_cells, :556-584), sort keys (padding keys sort last)
-            // and each geom's staged centre, radius, body, type and masks.
+            uint32_t* const hmeta = (uint32_t*)(s.hpos + a.G);
+            // Cells (broad_phase_count_cells, :556-584), sort keys and each geom's staged
+            // centre, radius and compact word. Up to 1024 keys are sorted in registers, which
+            // pad the list themselves, so only the G real keys are stored; a longer list is
+            // padded to Gp in LDS (padding keys sort last).
+            const uint32_t nkeys = a.Gp <= 1024u ? a.G : a.Gp;
             if (live) {
-                for (uint32_t g = sl; g < a.Gp; g += G) {
+                for (uint32_t g = sl; g < nkeys; g += G) {
                     uint32_t key = 0xFFFFFFFFu;
                     if (g < a.G) {
                         const GeomRec& gr = md.geoms[g];
                         const f3 p = add(xyz(s.pos[gr.type_body[1]]), mk3(gr.pos_size0[0], gr.pos_size0[1], gr.pos_size0[2]));
                         const uint32_t id = hash_axis(p.x) + hash_axis(p.y) * 64u + hash_axis(p.z) * 4096u;
-                        s.hcell[g] = id;
                         if (HBM) {
                             s.hpos[g] = tof4(p, gr.pos_size0[3]);
-                            hmeta[g] = make_uint4(gr.type_body[1], gr.type_body[0], gr.type_body[2], gr.type_body[3]);
+                            hmeta[g] = md.hmeta[g];
                         }
                         a.cell_ids[(size_t)env * a.G + g] = id;
                         key = (id << 14) | g;
@@ -1549,10 +1593,10 @@ void step_kernel(StepArgs a) {
                 }
             }
             wave_sync<HBM>();
-            // Bitonic sort of the Gp keys: up to 1024 in registers (sixteen per lane), more in
+            // Bitonic sort of the keys: up to 1024 in registers (sixteen per lane), more in
             // LDS, one compare-exchange pair per lane and pass.
             if (a.Gp <= 1024u) {
-                if (live) sort_keys_1024(s.hkey, a.Gp, (uint32_t)sl);
+                if (live) sort_keys_1024(s.hkey, a.G, (uint32_t)sl);
                 wave_sync<HBM>();
             } else
             for (uint32_t k = 2; k <= a.Gp; k <<= 1) {
@@ -1586,8 +1630,20 @@ void step_kernel(StepArgs a) {
                     if ((uint32_t)sl >= d) inc += t;
                 }
                 const uint32_t total = __shfl(inc, G - 1, G);
-                if (mine && h > 0 && count + (inc - h) < M) hash_pairs_of<HBM>(a, md, s, hmeta, g, true, count + (inc - h));
+                // The geom's pairs take slots start .. start + h - 1 in u32 arithmetic: some land
+                // below M if the first does, or if they wrap the count past 2^32 (then from 0).
+                const uint32_t start = count + (inc - h);
+                if (mine && h > 0 && (start < M || (uint64_t)start + h > 0xFFFFFFFFull))
+                    hash_pairs_of<HBM>(a, md, s, hmeta, g, true, start);
                 count += total;
+            }
+            if (LATE_SNAP) {  // the hash's arrays are dead: the snapshot takes their place
+                wave_sync<HBM>();
+                if (live && snap_first) {
+                    for (uint32_t k = sl; k < (pcount < M ? pcount : M); k += G) { s.ppen[k] = hppen[k]; s.pimp[k] = hpimp[k]; }
+                } else if (live) {
+                    snapshot(count_before, s.ppen, s.pimp);
+                }
             }
         } else if (EPW == 1 && live && a.sweep_n != 0u && count >= M && count <= 0xFFFFFFFFu - a.P) {
             // Count-only sweep. The list is full (count >= M) and this substep cannot wrap

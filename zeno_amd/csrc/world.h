@@ -42,6 +42,7 @@ struct World {
     EnvLds lds{};
     EnvLds lds_small{};  // placement 2: the arrays kept in LDS
     bool hash = false;  // spatial-hash broad phase (more than kHashMinGeoms geoms)
+    bool hrows = false;  // hash filter classes fit the model's rows (build_hash_words)
     uint32_t placement = PL_LDS;  // where the step kernel keeps model records and working sets
     bool ext_contacts = false;    // extended-contact mode (zeno_amd_world_set_extended_contacts)
     bool resort = false;          // counts set by the host: the next launch sorts unconditionally

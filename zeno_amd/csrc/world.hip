@@ -299,6 +299,12 @@ World* World::create(const Scene& scene, const ZenoConfig& cfg, std::string& err
         build_body_joint_lists(m.joints, w->B, bjoff, bjl);
         put(w->ml.bjoff, bjoff.data(), 4 * bjoff.size());
         put(w->ml.bjl, bjl.data(), 4 * bjl.size());
+        if (w->hash) {
+            std::vector<uint32_t> hmeta, hrow;
+            w->hrows = build_hash_words(m.geoms, hmeta, hrow);
+            put(w->ml.hmeta, hmeta.data(), 4 * hmeta.size());
+            put(w->ml.hrow, hrow.data(), 4 * hrow.size());
+        }
         if ((e = upload(w, &w->d_model, (const uint4*)blob.data(), w->ml.bytes / 16)) != hipSuccess) return fail("upload", e);
     }
     if (!w->hash && !m.pairs.empty()) {
@@ -402,6 +408,7 @@ hipError_t World::launch(const float* d_act, uint32_t substeps, const uint8_t* d
     a.E = E; a.B = B; a.J = J; a.Jp = Jp; a.A = A; a.S = model.num_sensors; a.obsp = obsp; a.N = N;
     a.nrec = nrec; a.njph = njph; a.M = M; a.P = model.num_pairs;
     a.G = model.num_geoms; a.Gp = hash ? hash_pad(model.num_geoms) : 0; a.hash = hash ? 1u : 0u;
+    a.hrows = hrows ? 1u : 0u;
     a.cell_ids = d_cell_ids;
     a.ext_contacts = ext_contacts ? 1u : 0u;
     a.sort_all = resort ? 1u : 0u;
